@@ -1,0 +1,225 @@
+"""Decode throughput of the MI355X Qwen3-4B engine (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
+
+Default workload is BASELINE.json's configs[1] ("c2"): Qwen3-4B, random-init
+bf16 weights (seed 0), batch 1, a 128-token uniform-random prompt, greedy
+decoding. The engine's own generate() runs the prompt forward (untimed) and
+W warm-up steps, then K decode steps are timed between two device
+synchronisations; ``value`` = decoded tokens / wall seconds over the steps
+launched inside that window. Inputs and weights are resident in HBM
+throughout; only token ids cross PCIe (8 bytes per sequence per step).
+
+Extra fields: ``roofline`` for the dominant kernel (the fused
+RMSNorm + gate/up GEMM + SwiGLU, 44% of the bytes of a B=1 step), timed live
+with HIP events on the stream it is launched on, rotating over the 36 layers'
+weights so that nothing is served from the 256 MB Infinity Cache;
+``step_roofline`` for the whole step (algorithmic bytes of weights + visible
+KV per step over the measured step time); ``cpu_baseline``: the oracle's
+torch-CPU restatement of the same decode step on this host's cores, over a
+bounded sample (2 of the 36 layers + the LM head, scaled to 36 layers).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "thing-htn-2026_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s
+CONFIGS = {
+    # name: (B, prompt length, decode steps), BASELINE.json configs[1..4]
+    "c2": (1, 128, 256),
+    "c3": (8, 2048, 512),
+    "c4": (32, 8192, 256),
+}
+QWEN3_4B = {
+    "hidden_size": 2560, "intermediate_size": 9728, "vocab_size": 151936,
+    "num_hidden_layers": 36, "num_attention_heads": 32, "num_key_value_heads": 8,
+    "head_dim": 128, "rms_norm_eps": 1e-6, "rope_theta": 5000000.0, "rope_scaling": None,
+    "tie_word_embeddings": True,
+}
+
+
+def weight_bytes(cfg) -> int:
+    H, I, D, Nq, Nkv, L, V = (cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"],
+                              cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["num_hidden_layers"],
+                              cfg["vocab_size"])
+    per_layer = 2 * (H * (Nq + 2 * Nkv) * D + Nq * D * H + 2 * I * H + I * H)
+    norms = 2 * (L * (2 * H + 2 * D) + H)
+    return L * per_layer + 2 * V * H + norms
+
+
+def kv_bytes_per_token(cfg) -> int:
+    return cfg["num_hidden_layers"] * 2 * cfg["num_key_value_heads"] * cfg["head_dim"] * 2
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-layers", type=int, default=2)
+    return p.parse_args()
+
+
+def time_dominant_kernel(eng, torch, reps_per_layer=3):
+    """Average duration of the fused norm + gate/up + SwiGLU GEMM at the bench's M."""
+    from qwen_hip import ops
+    B = eng.B
+    b = eng._buffers(B, 1)
+    h, p = b["h"], b["p"]
+    stream = torch.cuda.current_stream()
+    for w in eng.layers[:2]:
+        ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    n = 0
+    for _ in range(reps_per_layer):
+        for w in eng.layers:
+            ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p)
+            n += 1
+    end.record(stream)
+    end.synchronize()
+    avg_s = start.elapsed_time(end) / 1e3 / n
+    w0 = eng.layers[0].w_gu
+    bytes_launch = w0.nbytes + B * w0.K * 2 + w0.K * 2 + B * (w0.N // 2) * 2
+    return avg_s, bytes_launch
+
+
+def cpu_baseline(eng, cfg, B, S, layers):
+    """Time the oracle's torch-CPU decode step on a 2-layer slice of the same weights."""
+    import torch
+    from oracle.model import CpuQwen3
+
+    def untile(t):
+        return t.data.view(t.N // 16, t.K // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(t.N, t.K).cpu()
+
+    lw = []
+    for w in eng.layers[:layers]:
+        lw.append({"ln1": w.ln1.cpu(), "ln2": w.ln2.cpu(), "q_norm": w.q_norm.cpu(), "k_norm": w.k_norm.cpu(),
+                   "w_qkv": w.r_qkv.cpu(), "w_o": w.r_o.cpu(), "w_gu": w.r_gu.cpu(), "w_down": w.r_down.cpu()})
+    weights = {"embed": untile(eng.embed), "final_norm": eng.final_norm.cpu(), "layers": lw}
+    ref = CpuQwen3(dict(cfg, num_hidden_layers=layers), weights)
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    ref.prepare(B, ((S + 64 + 63) // 64) * 64)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    with torch.inference_mode():
+        ref.prefill(ids)
+        ref.hist[:, :S] = ids
+        ref.pos.fill_(S - 1)
+        ref.plain_step()                       # warm-up
+        t_layers, t_head, steps = 0.0, 0.0, 0
+        t_end = time.perf_counter() + 15.0
+        while time.perf_counter() < t_end or steps < 2:
+            tok = ref.hist.gather(1, ref.pos.to(torch.int64)[:, None])
+            t0 = time.perf_counter()
+            h = ref.w["embed"][tok.reshape(-1)]
+            d = None
+            for l in range(layers):
+                h, d = ref.layer(l, h, d, ref.pos, 1, B)
+            t1 = time.perf_counter()
+            from oracle import ref_torch as R
+            _, n = R.add_rms_norm(h, d, ref.w["final_norm"], ref.eps)
+            R.argmax_lowest(R.linear(n, ref.w["embed"]))
+            t2 = time.perf_counter()
+            ref.pos += 1
+            t_layers += t1 - t0
+            t_head += t2 - t1
+            steps += 1
+    per_token = (t_layers / steps) * cfg["num_hidden_layers"] / layers + t_head / steps
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(B / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle torch-CPU decode step (oracle/model.py) on {layers} of "
+                       f"{cfg['num_hidden_layers']} layers + LM head, {steps} steps at context ~{S}, "
+                       f"scaled to {cfg['num_hidden_layers']} layers; host CPU {cpu}")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build runs on a single MI355X); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from __graft_entry__ import write_random_model
+    from engine import Engine
+
+    B, S, N = CONFIGS[args.config]
+    K = args.steps if args.steps is not None else N
+    W = args.warmup
+    cfg = QWEN3_4B
+    with tempfile.TemporaryDirectory() as d:
+        eng = Engine(write_random_model(d, cfg, seed=0, std=0.02))
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
+    total = 1 + W + K
+    gen = eng.generate(prompt, total)
+    t_pf = time.perf_counter()
+    next(gen)                                  # prompt forward + first token
+    ttft = time.perf_counter() - t_pf
+    for _ in range(W):
+        next(gen)
+    torch.cuda.synchronize()
+    l0 = eng.decode_launches
+    t0 = time.perf_counter()
+    for _ in gen:
+        pass
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    steps = eng.decode_launches - l0
+    dt = t1 - t0
+    tok_s = steps * B / dt
+    ms_step = dt / steps * 1e3
+
+    ctx_mid = S + 1 + W + steps / 2
+    step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
+    avg_s, k_bytes = time_dominant_kernel(eng, torch)
+    achieved = k_bytes / avg_s
+    out = {
+        "metric": "decode tok/s at B=1 (Qwen3-4B bf16)" if B == 1 else f"decode tok/s at B={B} (Qwen3-4B bf16)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (counter-based generator, seed 0, std 0.02), "
+                "uniform-random prompt ids (torch seed 1)",
+        "config": {"workload": f"{args.config}: Qwen3-4B, B={B}, prompt {S}, {N} greedy decode steps",
+                   "global_batch": B, "seq_len": S, "decode_steps": N, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "skinny_gemm norm+gate/up+SwiGLU (one layer)",
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "avg_us": round(avg_s * 1e6, 2), "bytes_per_launch": k_bytes},
+        "step_roofline": {"bytes_per_step": int(step_bytes), "achieved_GBps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
+                          "frac": round(step_bytes / (ms_step / 1e3) / HBM_PEAK, 4)},
+        "ttft_s": round(ttft, 3),
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(eng, cfg, B, S, args.cpu_layers)
+        except Exception as error:  # noqa: BLE001 - report, do not fail the GPU number
+            out["cpu_baseline"] = {"value": None, "error": repr(error)[:200]}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

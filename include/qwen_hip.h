@@ -1,0 +1,114 @@
+/*
+ * C ABI of libqwen_hip.so: the MI355X (gfx950) kernels behind the Qwen3-4B
+ * greedy-decode engine.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise; bf16 tensors
+ *     are raw 16-bit patterns, row-major and contiguous.
+ *   - Every entry point enqueues work on `stream` and returns immediately; it
+ *     never allocates, frees or synchronises, so it can be recorded into a
+ *     HIP graph. Return value: 0 on success, 1001 (bad size/shape argument),
+ *     1002 (null pointer), 1003 (workspace too small), otherwise the
+ *     hipError_t of the failed launch.
+ *   - "Tiled" weights use the MFMA-B tile layout written by
+ *     qwen_tile_weight / qwen_init_weight: tile (nt, kt) of 16 rows x 32
+ *     columns is 1 KB at element offset (nt * K/32 + kt) * 512, and lane
+ *     l = 16*q + r of a tile holds W[16*nt + r][32*kt + 8*q .. +8].
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference repository).
+ */
+#ifndef QWEN_HIP_H
+#define QWEN_HIP_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* rms_norm(x, w, eps) -> y.  x, y: [M, N] bf16; w: [N] bf16; N % 8 == 0, N <= 8192.
+ * Replaces engine/kernels/rmsnorm.py:141-167 (rms_norm) / torch_ref.py:47-58. */
+int qwen_rms_norm(const void* x, const void* w, void* y, int M, int N, float eps, hipStream_t stream);
+
+/* add_rms_norm(x, r, w, eps) -> (h, y): h = bf16(x + r), y = rms_norm(h).
+ * Replaces engine/kernels/rmsnorm.py:170-207 (add_rms_norm) / torch_ref.py:61-68. */
+int qwen_add_rms_norm(const void* x, const void* r, const void* w, void* h, void* y, int M, int N, float eps,
+                      hipStream_t stream);
+
+/* silu_mul(gu [M, 2I]) -> out [M, I] = bf16(bf16(silu(gate)) * up).
+ * Replaces engine/kernels/silu.py:95-125 (silu_mul) / torch_ref.py:74-88. */
+int qwen_silu_mul(const void* gu, void* out, int M, int I, hipStream_t stream);
+
+/* qk_norm_rope_cache(qkv [B*T, (Nq+2Nkv)*D], q_norm_w [D], k_norm_w [D], eps, cos/sin [P, D],
+ * positions [B] int32, T, k_cache/v_cache [B, Nkv, CAP, D]) -> q_out [B, T, Nq, D];
+ * writes K (normed + RoPE) and V at slots positions[b] + t (P = rows of the cos/sin tables;
+ * a slot outside [0, min(CAP, P)) is skipped, never written). D must be 128.
+ * Replaces engine/kernels/rope.py:169-226 (qk_norm_rope_cache) / torch_ref.py:107-162. */
+int qwen_qk_norm_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                            const void* sin_tab, const int32_t* positions, void* q_out, void* k_cache, void* v_cache,
+                            int B, int T, int Nq, int Nkv, int D, int CAP, int P, float eps, hipStream_t stream);
+
+/* Workspace bytes for qwen_attn_decode with the given split count. */
+long long qwen_attn_workspace_bytes(int B, int T, int Nq, int Nkv, int D, int num_splits);
+
+/* attn_decode(q [B, T, Nq, D], caches [B, Nkv, CAP, D], lengths [B] int32, scale, num_splits)
+ * -> out [B, T, Nq*D]. The valid length of sequence b is lengths[b] + len_add (len_add = 0
+ * gives the reference semantics; the engine passes positions with len_add = T).
+ * Nq == 4 * Nkv, D == 128, 1 <= T <= 16.
+ * Replaces engine/kernels/attention.py:278-348 (attn_decode) / torch_ref.py:168-227. */
+int qwen_attn_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* lengths, int len_add,
+                     void* out, void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
+                     int CAP, float scale, int num_splits, hipStream_t stream);
+
+/* out = x @ W^T with optional RMSNorm prologue (norm_w != NULL) and epilogue
+ * epi = 0 store, 1 residual add (out = bf16(residual + bf16(acc)); residual may alias out),
+ * 2 SwiGLU pair (W tiled with pair interleave; N = 2I rows; out has I columns).
+ * x: [M, K] (M <= 32), W tiled [N, K]. ntw (1|2) n-tiles and ksplit (1|2|4|8|16)
+ * wavefronts per workgroup select the launch shape.
+ * Replaces the projections of engine/engine.py:1108-1118 (_mm / F.linear) and
+ * engine/kernels/gemm_fused.py:136-173 (fused_linear). */
+int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* norm_w,
+                float eps, const void* residual, int epi, int ntw, int ksplit, hipStream_t stream);
+
+/* Workspace bytes for qwen_lm_head_argmax. */
+long long qwen_argmax_workspace_bytes(int M, int N, int ntw);
+
+/* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
+ * out_tok[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]).
+ * Replaces engine/engine.py:1119-1121 (final add_rms_norm, lm_head _mm, argmax). */
+int qwen_lm_head_argmax(const void* x, const void* norm_w, float eps, const void* w_tiled, int M, int N, int K,
+                        void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw, int ksplit,
+                        hipStream_t stream);
+
+/* Embedding gather from the tiled tied table: out[m] = W[tok[m]], or, with tok == NULL,
+ * out[m] = W[hist[m, pos[m]]] (the decode step's token read, engine/engine.py:941-946).
+ * Replaces F.embedding at engine/engine.py:1101. */
+int qwen_embed(const int64_t* tok, const int64_t* hist, const int32_t* pos, int cap, const void* w_tiled, void* out,
+               int M, long long V, int K, hipStream_t stream);
+
+/* Token bookkeeping after a plain decode step: hist[b, pos[b]+1] = next[b], pos[b] += 1,
+ * frozen rows ((pos+1 - s_buf) >= ntarget) write slot cap-1 and keep pos.
+ * Replaces the tail of engine/engine.py:941-953 (_plain_step). */
+int qwen_plain_update(const int64_t* next, int64_t* hist, int32_t* pos, const int64_t* s_buf, const int64_t* ntarget,
+                      int B, int cap, hipStream_t stream);
+
+/* Row-major [N, K] bf16 -> tiled layout (pair = 1: gate|up interleave, tile 2p = rows
+ * 16p.., tile 2p+1 = rows N/2 + 16p..). Replaces the weight fusion / layout step of
+ * engine/engine.py:209-227 (the reference keeps row-major; this build re-lays for MFMA). */
+int qwen_tile_weight(const void* src, void* dst, long long N, int K, int pair, hipStream_t stream);
+
+/* Fill a [N, K] weight (tiled != 0: tiled layout) from the counter-based random-init
+ * generator: nseg row segments starting at seg_start[i] (host array, ascending, first 0)
+ * drawn from tensor ids seg_tid[i]; element = bf16(f32(IrwinHall4(splitmix64(seed<<52 |
+ * tid<<32 | local_index)) - 131070) * scale). No reference counterpart: the benchmark
+ * configs' "random-init weights from seed 0" (HF init would run on the host). */
+int qwen_init_weight(void* dst, long long N, int K, int tiled, int pair, const int* seg_start, const int* seg_tid,
+                     int nseg, unsigned long long seed, float scale, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_HIP_H */

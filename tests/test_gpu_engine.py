@@ -1,0 +1,157 @@
+"""GPU tests of the drop-in Engine: protocol, state handling and greedy parity with the CPU oracle.
+
+The parity rule is the reference judge's (``tests/local_check.py:254-271``),
+teacher-forced on the engine's own tokens, with the margin tightened from 2.0
+logits to one bf16 ulp at the logit magnitude (a token may differ from the
+oracle's argmax only inside a bf16 near-tie). Protocol and state cases mirror
+``tests/local_check.py:47-54`` and ``:197-230``.
+"""
+
+import itertools
+
+import pytest
+import torch
+
+from __graft_entry__ import write_random_model
+from oracle.model import QWEN3_4B, CpuQwen3
+
+pytestmark = pytest.mark.gpu
+
+SMALL = {
+    "hidden_size": 512, "intermediate_size": 1024, "vocab_size": 2048, "num_hidden_layers": 3,
+    "num_attention_heads": 8, "num_key_value_heads": 2, "head_dim": 128, "rms_norm_eps": 1e-6,
+    "rope_theta": 5000000.0, "rope_scaling": None, "tie_word_embeddings": True,
+}
+STD = 0.05
+
+
+def _prompt(B, S, V, seed):
+    g = torch.Generator().manual_seed(seed * 1_000_003 + 7_919 + 1)
+    return torch.randint(0, V, (B, S), generator=g).tolist()
+
+
+def _run(engine, prompt, N, V):
+    steps = list(itertools.islice(engine.generate([list(r) for r in prompt], N), N + 1))
+    assert len(steps) == N, f"yielded {len(steps)} steps, expected {N}"
+    B = len(prompt)
+    for s in steps:
+        assert isinstance(s, list) and len(s) == B
+        assert all(type(t) is int and 0 <= t < V for t in s)
+    return [[steps[n][b] for n in range(N)] for b in range(B)]
+
+
+@pytest.fixture(scope="module")
+def small(tmp_path_factory):
+    from engine import Engine
+    path = write_random_model(str(tmp_path_factory.mktemp("small")), SMALL, seed=0, std=STD)
+    return Engine(path), CpuQwen3.random_init(SMALL, seed=0, std=STD)
+
+
+@pytest.mark.parametrize("B,S,N", [(1, 5, 4), (2, 17, 6), (3, 64, 4), (1, 130, 9), (8, 40, 5)])
+def test_generate_matches_oracle(small, B, S, N):
+    eng, ref = small
+    prompt = _prompt(B, S, SMALL["vocab_size"], B * 100 + S)
+    tokens = _run(eng, prompt, N, SMALL["vocab_size"])
+    gaps = ref.judge_gaps(prompt, tokens)
+    assert float(gaps.max()) <= 0.0625, f"worst gap {float(gaps.max())}"
+
+
+def test_state_leak_and_batch_change(small):
+    eng, ref = small
+    V = SMALL["vocab_size"]
+    for i, (name, B, S, N) in enumerate([("leak-1", 2, 17, 6), ("leak-2", 2, 17, 6), ("bchange-3", 3, 17, 6),
+                                         ("bchange-1", 1, 17, 6)]):
+        prompt = _prompt(B, S, V, 500 + i)
+        tokens = _run(eng, prompt, N, V)
+        assert float(ref.judge_gaps(prompt, tokens).max()) <= 0.0625, name
+
+
+def test_zero_and_one_tokens(small):
+    eng, _ = small
+    assert list(eng.generate([[1, 2, 3]], 0)) == []
+    out = list(eng.generate([[1, 2, 3]], 1))
+    assert len(out) == 1 and len(out[0]) == 1
+
+
+def test_rejects_bad_token_ids(small):
+    eng, _ = small
+    with pytest.raises(ValueError):
+        list(eng.generate([[1, SMALL["vocab_size"]]], 2))
+
+
+def test_exactly_n_minus_one_decode_steps(small, monkeypatch):
+    """``tests/launch_count.py:57-65``: plain decoding launches exactly N-1 steps."""
+    eng, _ = small
+    import engine as engine_mod
+    monkeypatch.setitem(engine_mod.CONFIG, "graphs", False)
+    eng.graphs = {}       # the next generate() with graphs on captures afresh
+    calls = {"n": 0}
+    real = eng._plain_step
+
+    def counted():
+        calls["n"] += 1
+        return real()
+
+    monkeypatch.setattr(eng, "_plain_step", counted)
+    _run(eng, _prompt(2, 9, SMALL["vocab_size"], 3), 7, SMALL["vocab_size"])
+    assert calls["n"] == 6
+
+
+def test_verify_step_matches_plain_steps(small):
+    """A T=5 verify forward (speculative-verify shape) gives each position's greedy token."""
+    eng, ref = small
+    B, S, T = 4, 33, 5
+    V = SMALL["vocab_size"]
+    prompt = _prompt(B, S, V, 77)
+    tokens = _run(eng, prompt, 1, V)
+    g = torch.Generator().manual_seed(2)
+    drafts = torch.randint(0, V, (B, T - 1), generator=g)
+    tok = torch.cat([torch.tensor(tokens), drafts], 1)           # [B, T]: accepted token + 4 drafts
+    eng.pos_buf.fill_(S)
+    got = eng.verify_step(tok).cpu()
+    ref.prepare(B, eng.CAP)
+    ref.prefill(torch.tensor(prompt))
+    pos = torch.full((B,), S, dtype=torch.int32)
+    _, logits = ref.step(tok, pos, T, return_logits=True)
+    logits = logits.float().view(B, T, -1)
+    gap = logits.amax(-1) - logits.gather(-1, got[..., None])[..., 0]
+    assert float(gap.max()) <= 0.0625
+
+
+@pytest.fixture(scope="module")
+def qwen4b_two_layers(tmp_path_factory):
+    """The real Qwen3-4B shapes (H 2560, I 9728, V 151936, 32/8 heads) with 2 layers."""
+    from engine import Engine
+    cfg = dict(QWEN3_4B, num_hidden_layers=2)
+    path = write_random_model(str(tmp_path_factory.mktemp("q4b2")), cfg, seed=0, std=0.02)
+    return Engine(path), CpuQwen3.random_init(cfg, seed=0, std=0.02), cfg
+
+
+def test_qwen4b_shapes_hidden_states(qwen4b_two_layers):
+    """Per-layer hidden states within 2e-2 relative (the parity bar for hidden states)."""
+    eng, ref, cfg = qwen4b_two_layers
+    B, S = 2, 24
+    prompt = _prompt(B, S, cfg["vocab_size"], 5)
+    _run(eng, prompt, 1, cfg["vocab_size"])           # prefill + state
+    hidden = []
+    tok = torch.tensor(prompt)[:, -1:]
+    eng.pos_buf.fill_(S - 1)                            # re-run the last prompt token as a decode step
+    with torch.inference_mode():
+        eng._step(1, tok=tok.to(eng.device), hidden=hidden)
+    ref.prepare(B, eng.CAP)
+    ref.prefill(torch.tensor(prompt)[:, :S - 1])
+    want = []
+    ref.step(tok, torch.full((B,), S - 1, dtype=torch.int32), 1, hidden=want)
+    for l, (a, b) in enumerate(zip(hidden, want)):
+        a, b = a.float().cpu(), b.float()
+        rel = float((a - b).norm() / b.norm())
+        assert rel <= 2e-2, f"layer {l}: relative error {rel}"
+
+
+def test_qwen4b_shapes_greedy(qwen4b_two_layers):
+    eng, ref, cfg = qwen4b_two_layers
+    for B, S, N in [(1, 40, 6), (4, 17, 4)]:
+        prompt = _prompt(B, S, cfg["vocab_size"], B + S)
+        tokens = _run(eng, prompt, N, cfg["vocab_size"])
+        gaps = ref.judge_gaps(prompt, tokens)
+        assert float(gaps.max()) <= 0.0625, f"worst gap {float(gaps.max())}"

@@ -1,0 +1,286 @@
+"""GPU parity of every HIP operator against the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact where the op has no reduction or transcendental (residual add,
+V-cache copy, embedding gather, weight tiling / generation, argmax on
+two-hot inputs); at most one bf16 ulp on a small fraction of elements where
+only the fp32 reduction order or a transcendental's last fp32 bit can differ
+(RMSNorm, SwiGLU, RoPE); the reference's own tolerances elsewhere (attention
+atol 2e-2 as ``tests/test_torch_ref.py:264``; GEMMs atol 1e-2 / rtol 1/64 as
+the reference's op certification, ``engine/engine.py:425-429``).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close_ulp, assert_close
+from oracle import ref_torch as R
+from oracle import weights as OW
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+DEV = "cuda:0"
+EPS = 1e-6
+
+
+def _bf16(*shape, gen, scale=1.0):
+    return (torch.randn(*shape, generator=gen, dtype=torch.float32) * scale).to(BF16)
+
+
+@pytest.fixture(scope="module")
+def qops():
+    from qwen_hip import ops
+    return ops
+
+
+def _gain(n, gen):
+    return (1.0 + 0.5 * torch.randn(n, generator=gen)).to(BF16)
+
+
+# ---------------------------------------------------------------- norms / silu
+
+@pytest.mark.parametrize("rows,n", [(1, 128), (6, 2560), (37, 1024), (3, 96), (64, 2560)])
+def test_rms_norm(qops, rows, n):
+    g = torch.Generator().manual_seed(1234)
+    x, w = _bf16(rows, n, gen=g, scale=3.0), _gain(n, g)
+    got = qops.rms_norm(x.to(DEV), w.to(DEV), EPS).cpu()
+    assert_bf16_close_ulp(got, R.rms_norm(x, w, EPS), 1, 2e-3, "rms_norm")
+
+
+@pytest.mark.parametrize("rows,n", [(1, 128), (6, 2560), (37, 1024)])
+def test_add_rms_norm(qops, rows, n):
+    g = torch.Generator().manual_seed(4321)
+    x, r, w = _bf16(rows, n, gen=g, scale=3.0), _bf16(rows, n, gen=g, scale=3.0), _gain(n, g)
+    h, y = qops.add_rms_norm(x.to(DEV), r.to(DEV), w.to(DEV), EPS)
+    h_ref, y_ref = R.add_rms_norm(x, r, w, EPS)
+    assert torch.equal(h.cpu(), h_ref)   # no reduction: bit-exact
+    assert_bf16_close_ulp(y.cpu(), y_ref, 1, 2e-3, "add_rms_norm")
+
+
+def test_rms_norm_zero_row(qops):
+    x = torch.zeros(2, 2560, dtype=BF16)
+    w = torch.ones(2560, dtype=BF16)
+    assert torch.equal(qops.rms_norm(x.to(DEV), w.to(DEV), EPS).cpu(), x)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 64), (7, 3072), (13, 9728), (5, 300)])
+def test_silu_mul(qops, rows, inter):
+    g = torch.Generator().manual_seed(42)
+    gu = _bf16(rows, 2 * inter, gen=g, scale=4.0)
+    got = qops.silu_mul(gu.to(DEV)).cpu()
+    assert_bf16_close_ulp(got, R.silu_mul(gu), 1, 2e-3, "silu_mul")
+
+
+# ---------------------------------------------------------------- rope + cache
+
+@pytest.mark.parametrize("B,T,positions,NQ,NKV", [(2, 1, [5, 40], 8, 2), (2, 3, [0, 17], 8, 2),
+                                                   (2, 9, [0, 0], 8, 2), (1, 1, [511], 32, 8),
+                                                   (4, 5, [4096, 100, 7, 2000], 32, 8)])
+def test_qk_norm_rope_cache(qops, B, T, positions, NQ, NKV):
+    g = torch.Generator().manual_seed(7)
+    D, CAP = 128, 4160
+    cos, sin = R.rope_tables(8192, 5e6, D)
+    qkv = _bf16(B * T, (NQ + 2 * NKV) * D, gen=g, scale=2.0)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    qw, kw = _gain(D, g), _gain(D, g)
+    pos = torch.tensor(positions, dtype=torch.int32)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    q_ref = R.qk_norm_rope_cache(qkv, qw, kw, EPS, cos, sin, pos, T, kc_ref, vc_ref)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    q = qops.qk_norm_rope_cache(qkv.to(DEV), qw.to(DEV), kw.to(DEV), EPS, cos.to(DEV), sin.to(DEV), pos.to(DEV),
+                                T, kd, vd)
+    assert q.shape == (B, T, NQ, D)
+    # RoPE's bf16(p1 + p2) can cancel, so a one-ulp difference in the normed input (fp32
+    # reduction order of the sum of squares) can move a near-zero output by several ulps:
+    # use the reference's op-certification tolerance (engine/engine.py:425-429) and bound
+    # the fraction of elements that differ at all.
+    for got, want, name in ((q.cpu(), q_ref, "q"), (kd.cpu(), kc_ref, "k_cache")):
+        assert_close(got, want, 1e-2, 1 / 64, name)
+        assert float((got != want).float().mean()) <= 1e-2, name
+    assert torch.equal(vd.cpu(), vc_ref)    # V is copied raw; every other slot untouched
+
+
+# ---------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("B,T,lengths,CAP,splits", [
+    (2, 1, [13, 40], 64, 1), (2, 1, [64, 64], 64, 4), (2, 3, [13, 40], 64, 2), (2, 3, [64, 30], 64, 1),
+    (1, 1, [513], 640, 8), (4, 5, [4101, 33, 5, 1000], 4160, 64), (3, 16, [16, 200, 1000], 1024, 16),
+    (8, 1, [2304, 1, 77, 2048, 999, 1500, 64, 65], 2368, 32)])
+def test_attn_decode(qops, B, T, lengths, CAP, splits):
+    g = torch.Generator().manual_seed(99)
+    NQ, NKV, D = 32, 8, 128
+    q = _bf16(B, T, NQ, D, gen=g)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    lens = torch.tensor(lengths, dtype=torch.int32)
+    want = R.attn_decode(q, kc, vc, lens, D ** -0.5)
+    got = qops.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), lens.to(DEV), D ** -0.5, splits).cpu()
+    assert got.shape == (B, T, NQ * D)
+    assert_close(got, want, 2e-2, 0, "attn")
+
+
+def test_attn_split_invariance_and_poison(qops):
+    g = torch.Generator().manual_seed(5)
+    B, T, NQ, NKV, D, CAP = 2, 3, 32, 8, 128, 512
+    lengths = [300, 77]
+    q = _bf16(B, T, NQ, D, gen=g).to(DEV)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    for b in range(B):
+        kc[b, :, lengths[b]:] = float("nan")
+        vc[b, :, lengths[b]:] = float("inf")
+    kc, vc = kc.to(DEV), vc.to(DEV)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    outs = [qops.attn_decode(q, kc, vc, lens, D ** -0.5, s).float().cpu() for s in (1, 2, 8, 32)]
+    for o in outs:
+        assert torch.isfinite(o).all()
+        assert_close(o, outs[0], 2e-2, 0, "split invariance")
+
+
+def test_attn_single_key_returns_value_exactly(qops):
+    g = torch.Generator().manual_seed(11)
+    B, NQ, NKV, D, CAP = 2, 32, 8, 128, 64
+    q = _bf16(B, 1, NQ, D, gen=g)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    got = qops.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.ones(B, dtype=torch.int32, device=DEV),
+                           D ** -0.5, 4).cpu()
+    want = vc[:, :, 0, :][:, :, None, :].expand(B, NKV, NQ // NKV, D).reshape(B, 1, NQ * D)
+    assert torch.equal(got, want)
+
+
+def test_attn_kv_head_mapping(qops):
+    B, NQ, NKV, D, CAP = 1, 32, 8, 128, 8
+    q = torch.zeros(B, 1, NQ, D, dtype=BF16)
+    kc = torch.zeros(B, NKV, CAP, D, dtype=BF16)
+    vc = torch.zeros(B, NKV, CAP, D, dtype=BF16)
+    for kvh in range(NKV):
+        vc[0, kvh] = float(kvh + 1)
+    got = qops.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor([3], dtype=torch.int32, device=DEV),
+                           D ** -0.5, 1).cpu().view(B, 1, NQ, D)
+    for h in range(NQ):
+        assert torch.equal(got[0, 0, h], torch.full((D,), float(h // 4 + 1), dtype=BF16))
+
+
+# ---------------------------------------------------------------- weights
+
+@pytest.mark.parametrize("N,K,pair", [(64, 64, False), (6144, 2560, False), (256, 96, True)])
+def test_tile_weight_roundtrip_and_embed(qops, N, K, pair):
+    g = torch.Generator().manual_seed(3)
+    w = _bf16(N, K, gen=g)
+    t = qops.tile_weight(w.to(DEV), pair=pair)
+    flat = t.data.cpu().view(N // 16, K // 32, 4, 16, 8)   # [nt, kt, q, r, 8]
+    back = flat.permute(0, 3, 1, 2, 4).reshape(N, K)        # row 16nt + r, col 32kt + 8q + e
+    if pair:
+        Ih = N // 2
+        order = torch.cat([torch.arange(Ih).view(-1, 16), (Ih + torch.arange(Ih)).view(-1, 16)], 1).view(-1)
+        assert torch.equal(back, w[order])
+    else:
+        assert torch.equal(back, w)
+        tok = torch.randint(0, N, (5,), generator=g)
+        assert torch.equal(qops.embed(tok.to(DEV), t).cpu(), w[tok])
+
+
+@pytest.mark.parametrize("tiled", [False, True])
+def test_init_weight_matches_numpy_generator(qops, tiled):
+    N, K, seed, std = 96, 160, 0, 0.02
+    scale = float(OW.scale_f32(std))
+    starts, tids = [0, 64], [OW.tensor_id(3, "q_proj"), OW.tensor_id(3, "k_proj")]
+    dst = torch.empty(N * K, dtype=BF16, device=DEV)
+    qops.init_weight(dst, N, K, tiled, False, starts, tids, seed, scale)
+    want = np.concatenate([OW.gen_tensor_bits(seed, tids[0], (64, K), std),
+                           OW.gen_tensor_bits(seed, tids[1], (32, K), std)])
+    got = dst.cpu().view(torch.int16).numpy().view(np.uint16)
+    if tiled:
+        got = got.reshape(N // 16, K // 32, 4, 16, 8).transpose(0, 3, 1, 2, 4).reshape(N, K)
+    assert np.array_equal(got.reshape(N, K), want)
+
+
+# ---------------------------------------------------------------- GEMMs
+
+def _linear_case(qops, M, N, K, gen, norm=False, res=False, silu=False):
+    x = _bf16(M, K, gen=gen, scale=1.0)
+    w = _bf16(N, K, gen=gen, scale=0.05)
+    nw = _gain(K, gen) if norm else None
+    resid = _bf16(M, N // 2 if silu else N, gen=gen) if res else None
+    xin = R.rms_norm(x, nw, EPS) if norm else x
+    y = R.linear(xin, w)
+    want = R.silu_mul(y) if silu else y
+    if res:
+        want = (resid.float() + want.float()).to(BF16)
+    t = qops.tile_weight(w.to(DEV), pair=silu)
+    got = qops.fused_linear(x.to(DEV), t, norm_w=None if nw is None else nw.to(DEV), eps=EPS,
+                            residual=None if resid is None else resid.to(DEV), silu_pair=silu).cpu()
+    return got, want
+
+
+@pytest.mark.parametrize("M", [1, 2, 8, 16, 20, 32])
+@pytest.mark.parametrize("kind", ["plain", "norm", "res", "silu"])
+def test_fused_linear(qops, M, kind):
+    g = torch.Generator().manual_seed(100 + M)
+    N, K = (512, 2560) if kind != "res" else (256, 4096)
+    got, want = _linear_case(qops, M, N, K, g, norm=kind in ("norm", "silu"), res=kind == "res",
+                             silu=kind == "silu")
+    assert_close(got, want, 1e-2, 1 / 64, kind)
+
+
+@pytest.mark.parametrize("ntw,ks", [(1, 1), (1, 2), (1, 4), (1, 8), (1, 16), (2, 1), (2, 4), (2, 8)])
+def test_fused_linear_launch_shapes_agree(qops, ntw, ks):
+    g = torch.Generator().manual_seed(9)
+    M, N, K = 5, 256, 9728
+    x, w = _bf16(M, K, gen=g), _bf16(N, K, gen=g, scale=0.05)
+    t = qops.tile_weight(w.to(DEV))
+    got = qops.fused_linear(x.to(DEV), t, cfg=(ntw, ks)).cpu()
+    assert_close(got, R.linear(x, w), 1e-2, 1 / 64, f"ntw={ntw} ks={ks}")
+
+
+def test_fused_linear_two_hot_exact(qops):
+    """Each output is a sum of two exactly representable products, so it is exact in any
+    order: the expected bf16 bits are closed-form (``gemm_fused.py:227-277``)."""
+    M, N, K = 3, 64, 256
+    g = torch.Generator().manual_seed(17)
+    x = torch.randint(-8, 9, (M, K), generator=g).to(BF16)
+    w = torch.zeros(N, K, dtype=BF16)
+    cols = torch.randint(0, K, (N, 2), generator=g)
+    for n in range(N):
+        w[n, cols[n, 0]] += 0.5
+        w[n, cols[n, 1]] += 0.25
+    want = (x.double() @ w.double().T).to(BF16)
+    got = qops.fused_linear(x.to(DEV), qops.tile_weight(w.to(DEV))).cpu()
+    assert torch.equal(got, want)
+
+
+# ---------------------------------------------------------------- LM head + argmax
+
+def test_lm_head_argmax_one_hot_exact(qops):
+    """Rows of W are one-hot: logits equal exact (normed) inputs; ties resolve to the lowest index."""
+    M, V, K = 4, 4096, 256
+    g = torch.Generator().manual_seed(21)
+    x = _bf16(M, K, gen=g)
+    nw = torch.ones(K, dtype=BF16)
+    w = torch.zeros(V, K, dtype=BF16)
+    w[torch.arange(V), torch.arange(V) % K] = 1.0      # logit[v] = n[v % K]: every value repeats
+    n = R.rms_norm(x, nw, EPS)
+    logits = R.linear(n, w)
+    want = logits.argmax(-1)
+    assert bool((want < K).all())                       # torch's first-index rule
+    got = qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, qops.tile_weight(w.to(DEV))).cpu()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M", [1, 4, 20, 32])
+def test_lm_head_argmax_random(qops, M):
+    V, K = 151936, 2560
+    g = torch.Generator().manual_seed(31 + M)
+    x = _bf16(M, K, gen=g)
+    nw = _gain(K, g)
+    w = _bf16(V, K, gen=g, scale=0.02)
+    logits = R.linear(R.rms_norm(x, nw, EPS), w).float()
+    got = qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, qops.tile_weight(w.to(DEV))).cpu()
+    top = logits.max(-1).values
+    chosen = logits.gather(-1, got[:, None])[:, 0]
+    # Identical unless the oracle's top-2 gap is within one bf16 ulp of the max.
+    ulp = torch.tensor([2.0 ** (math.floor(math.log2(abs(float(t)))) - 7) for t in top])
+    assert bool(((top - chosen) <= ulp).all())
+    exact = (top - logits.topk(2, -1).values[:, 1]) > 2 * ulp
+    assert torch.equal(got[exact], logits.argmax(-1)[exact])

@@ -1,0 +1,83 @@
+// Shared device helpers for the Qwen3 decode kernels (gfx950 / CDNA4).
+//
+// bf16 values travel as raw 16-bit patterns (uint16_t). Conversions are done
+// by hand so every rounding point is explicit: widening is exact (<< 16),
+// narrowing is IEEE round-to-nearest-even on the fp32 bit pattern.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+#define QWEN_WAVE 64
+
+// Status codes returned by every C-ABI entry point (0 = success). Positive
+// values below 1000 are hipError_t codes from the launch.
+enum {
+  QWEN_OK = 0,
+  QWEN_EARG = 1001,      // a size / shape argument is out of the supported range
+  QWEN_ENULL = 1002,     // a required pointer is null
+  QWEN_EWORKSPACE = 1003 // caller-provided workspace is too small
+};
+
+__device__ __forceinline__ float bf2f(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// fp32 -> bf16, round to nearest, ties to even. NaN stays NaN (quiet).
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// Round an fp32 value to the nearest bf16 and return it widened again.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Product / sum with no contraction into an FMA: the reference rounds each
+// square before summing it (and torch's CPU kernels do the same).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+// Unpack 8 bf16 held in a uint4 (little-endian pairs) to fp32.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+  v.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+  v.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+  v.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  return v;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Wave-wide sum / max with a fixed butterfly order (deterministic).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, QWEN_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QWEN_WAVE));
+  return v;
+}
+
+static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
+
+// Launch-status check used by every entry point: returns the launch error.
+#define QWEN_RETURN_LAUNCH() return qwen_status(hipGetLastError())

@@ -1,0 +1,509 @@
+"""Qwen3-4B greedy-decode engine for one MI355X (gfx950): drop-in for the reference's ``engine/engine.py``.
+
+Same public surface as the reference (``engine/engine.py:109-111``,
+``:1225-1250``): ``Engine(model_path)`` loads the model once; then
+``generate(input_ids, max_new_tokens)`` is a generator that yields exactly
+``max_new_tokens`` lists of ``B`` Python ints, the first from the prompt
+forward, then one per decode step. State resets on every call; batch size and
+prompt length may change between calls.
+
+Per decode step the device runs only hand-written HIP kernels from
+``qwen_hip`` (libqwen_hip.so), recorded once per batch shape into one HIP
+graph (``torch.cuda.CUDAGraph``) and replayed per token:
+
+    embed(hist[pos])                                   1 kernel
+    36 x [ norm+QKV GEMM | QK-norm+RoPE+KV write |
+           split-K attention (partial + merge) |
+           O GEMM + residual | norm+gate/up GEMM+SwiGLU |
+           down GEMM + residual ]                      7 kernels / layer
+    final norm + LM head + argmax                      2 kernels
+    history / position update                          1 kernel
+
+Torch is used for device memory, the KV cache, the RoPE tables, graph
+capture, host<->device copies and (for now) the prompt forward's large GEMMs
+and causal attention (hipBLASLt / SDPA flash), whose norms, RoPE, cache writes
+and SwiGLU are the same HIP kernels. There is no CPU fallback: without a GPU
+or without libqwen_hip.so the constructor raises.
+"""
+
+from __future__ import annotations
+
+import glob
+import json
+import math
+import os
+import sys
+import time
+from collections import deque
+
+import torch
+import torch.nn.functional as F
+
+from qwen_hip import ops
+from qwen_hip.ops import TiledWeight
+
+BF16 = torch.bfloat16
+
+CONFIG = {
+    "graphs": True,          # replay one HIP graph per decode step
+    "pipeline_depth": 3,     # decode steps in flight ahead of the host yield (engine/engine.py:71)
+    "prefill_rows": 32768,   # max B*S rows per prompt-forward batch slice (engine/engine.py:72)
+    "cap_align": 64,         # KV-cache capacity alignment (engine/engine.py:73)
+    "log": True,
+}
+
+# Tensor ids of the counter-based random-init generator (one per HF weight).
+_PROJ_IDS = {"q_proj": 0, "k_proj": 1, "v_proj": 2, "o_proj": 3, "gate_proj": 4, "up_proj": 5, "down_proj": 6}
+
+
+def _log(*parts):
+    if CONFIG["log"]:
+        print("[engine]", *parts, file=sys.stderr, flush=True)
+
+
+def _tid(layer, name):
+    return 0 if name == "embed" else 1 + 16 * layer + _PROJ_IDS[name]
+
+
+def random_init_scale(std: float) -> float:
+    """fp32 multiplier of the centred Irwin-Hall(4) sum of 16-bit fields (sigma^2 = (2^32 - 1) / 3)."""
+    import numpy as np
+    return float(np.float32(std / math.sqrt((65536.0 * 65536.0 - 1.0) / 3.0)))
+
+
+class _Layer:
+    __slots__ = ("ln1", "w_qkv", "q_norm", "k_norm", "w_o", "ln2", "w_gu", "w_down",
+                 "r_qkv", "r_o", "r_gu", "r_down")
+
+
+class Engine:
+    def __init__(self, model_path: str) -> None:
+        """Load the model from ``model_path`` (HF checkpoint dir, or config + random_init.json)."""
+        t0 = time.time()
+        if not torch.cuda.is_available():
+            raise RuntimeError("Engine needs an MI355X GPU (HIP device); there is no CPU path")
+        self.device = torch.device("cuda:0")
+        torch.backends.cuda.matmul.allow_tf32 = False
+        with open(os.path.join(model_path, "config.json")) as handle:
+            cfg = json.load(handle)
+        self.cfg = cfg
+        self.H = cfg["hidden_size"]
+        self.I = cfg["intermediate_size"]
+        self.V = cfg["vocab_size"]
+        self.L = cfg["num_hidden_layers"]
+        self.Nq = cfg["num_attention_heads"]
+        self.Nkv = cfg["num_key_value_heads"]
+        self.D = cfg.get("head_dim") or self.H // self.Nq
+        self.eps = float(cfg["rms_norm_eps"])
+        theta = cfg.get("rope_theta")
+        if theta is None:
+            theta = (cfg.get("rope_parameters") or {}).get("rope_theta")
+        self.theta = float(theta)
+        self.scale = self.D ** -0.5
+        rope_params = cfg.get("rope_parameters") or {}
+        if cfg.get("rope_scaling") is not None or rope_params.get("rope_type", "default") != "default":
+            raise RuntimeError("rope_scaling is not supported by this engine")
+        if self.D != 128 or self.Nq != 4 * self.Nkv:
+            raise RuntimeError(f"kernels support head_dim 128 and 4 query heads per KV head (got {self.D}, "
+                               f"{self.Nq}/{self.Nkv})")
+        if self.H % 32 or self.I % 32 or self.V % 16:
+            raise RuntimeError("hidden/intermediate sizes must be multiples of 32 and vocab of 16")
+        self.ops = {
+            "rms_norm": ops.rms_norm,
+            "add_rms_norm": ops.add_rms_norm,
+            "silu_mul": ops.silu_mul,
+            "qk_norm_rope_cache": ops.qk_norm_rope_cache,
+            "attn_decode": ops.attn_decode,
+        }
+        self.B = self.CAP = 0
+        self.graphs = {}
+        self.step_ms = {}
+        self.sdpa_mode = None
+        self.decode_launches = 0   # decode steps launched since load (benchmarks read it)
+        self._load_weights(model_path)
+        self._rope_max = 0
+        self._ensure_rope(8192)
+        torch.cuda.synchronize()
+        _log(f"loaded in {time.time() - t0:.1f}s: L={self.L} H={self.H} V={self.V}")
+
+    # ------------------------------------------------------------------ weights
+    def _load_weights(self, model_path):
+        rnd = os.path.join(model_path, "random_init.json")
+        if os.path.exists(rnd):
+            with open(rnd) as handle:
+                spec = json.load(handle)
+            self._init_random(int(spec.get("seed", 0)), float(spec.get("std", 0.02)))
+        else:
+            self._load_safetensors(model_path)
+
+    def _init_random(self, seed: int, std: float):
+        """Random-init weights on the device from the counter-based generator (tiled + row-major)."""
+        dev, H, I, D, Nq, Nkv = self.device, self.H, self.I, self.D, self.Nq, self.Nkv
+        scale = random_init_scale(std)
+        ones_h = torch.ones(H, dtype=BF16, device=dev)
+        ones_d = torch.ones(D, dtype=BF16, device=dev)
+        self.layers = []
+        for l in range(self.L):
+            w = _Layer()
+            w.ln1, w.ln2, w.q_norm, w.k_norm = ones_h.clone(), ones_h.clone(), ones_d.clone(), ones_d.clone()
+            qkv_seg = ([0, Nq * D, (Nq + Nkv) * D],
+                       [_tid(l, "q_proj"), _tid(l, "k_proj"), _tid(l, "v_proj")])
+            gu_seg = ([0, I], [_tid(l, "gate_proj"), _tid(l, "up_proj")])
+            shapes = {
+                "qkv": ((Nq + 2 * Nkv) * D, H, qkv_seg, False),
+                "o": (H, Nq * D, ([0], [_tid(l, "o_proj")]), False),
+                "gu": (2 * I, H, gu_seg, True),
+                "down": (H, I, ([0], [_tid(l, "down_proj")]), False),
+            }
+            for name, (N, K, (starts, tids), pair) in shapes.items():
+                setattr(w, "w_" + name, TiledWeight.random(N, K, starts, tids, seed, scale, dev, pair))
+                row = torch.empty((N, K), dtype=BF16, device=dev)
+                ops.init_weight(row, N, K, False, False, starts, tids, seed, scale)
+                setattr(w, "r_" + name, row)
+            self.layers.append(w)
+        self.embed = TiledWeight.random(self.V, H, [0], [_tid(None, "embed")], seed, scale, dev)
+        self.final_norm = ones_h.clone()
+
+    def _load_safetensors(self, model_path):
+        """HF Qwen3 checkpoint (safetensors, safe loader) -> fused, tiled device weights."""
+        from safetensors.torch import safe_open
+        files = sorted(glob.glob(os.path.join(model_path, "*.safetensors")))
+        if not files:
+            raise RuntimeError(f"no safetensors weights and no random_init.json in {model_path}")
+        tensors = {}
+        for f in files:
+            with safe_open(f, framework="pt", device="cpu") as handle:
+                for k in handle.keys():
+                    tensors[k] = handle.get_tensor(k)
+
+        def get(name):
+            return tensors[name].to(device=self.device, dtype=BF16).contiguous()
+
+        self.layers = []
+        for l in range(self.L):
+            p = f"model.layers.{l}."
+            w = _Layer()
+            w.ln1 = get(p + "input_layernorm.weight")
+            w.ln2 = get(p + "post_attention_layernorm.weight")
+            w.q_norm = get(p + "self_attn.q_norm.weight")
+            w.k_norm = get(p + "self_attn.k_norm.weight")
+            w.r_qkv = torch.cat([get(p + "self_attn.q_proj.weight"), get(p + "self_attn.k_proj.weight"),
+                                 get(p + "self_attn.v_proj.weight")], 0).contiguous()
+            w.r_o = get(p + "self_attn.o_proj.weight")
+            w.r_gu = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], 0).contiguous()
+            w.r_down = get(p + "mlp.down_proj.weight")
+            w.w_qkv = ops.tile_weight(w.r_qkv)
+            w.w_o = ops.tile_weight(w.r_o)
+            w.w_gu = ops.tile_weight(w.r_gu, pair=True)
+            w.w_down = ops.tile_weight(w.r_down)
+            self.layers.append(w)
+        emb = get("model.embed_tokens.weight")
+        self.embed = ops.tile_weight(emb)
+        if "lm_head.weight" in tensors and not self.cfg.get("tie_word_embeddings", True):
+            raise RuntimeError("untied LM head is not supported (Qwen3-4B ties it to the embedding)")
+        del emb
+        self.final_norm = get("model.norm.weight")
+        del tensors
+
+    def _ensure_rope(self, max_pos):
+        """cos/sin ``[P, D]`` bf16 with the reference's op sequence (``engine/engine.py:232-251``).
+
+        Computed on the host CPU so the table is bit-identical to the
+        Transformers rotary embedding on CPU, then copied to the device.
+        """
+        if max_pos <= self._rope_max:
+            return
+        P = int(2 ** math.ceil(math.log2(max(max_pos, 1024))))
+        inv_freq = 1.0 / (self.theta ** (torch.arange(0, self.D, 2, dtype=torch.int64).to(torch.float32) / self.D))
+        pos = torch.arange(P, dtype=torch.float32)[None, :]
+        freqs = (inv_freq[None, :, None].float().expand(1, -1, 1) @ pos[:, None, :].float()).transpose(1, 2)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        self.cos_tab = emb.cos()[0].to(BF16).contiguous().to(self.device)
+        self.sin_tab = emb.sin()[0].to(BF16).contiguous().to(self.device)
+        self._rope_max = P
+        self.graphs = {}  # captured graphs hold the old table addresses
+
+    # ------------------------------------------------------------------ state
+    def _prepare(self, B, S, N):
+        """Per-shape state (``engine/engine.py:830-863``): KV cache, history, buffers, graph."""
+        if B > 32:
+            raise ValueError("this engine decodes at most 32 sequences per call")
+        slack = (CONFIG["pipeline_depth"] + 3) + 16
+        align = CONFIG["cap_align"]
+        cap = ((S + N + slack + align - 1) // align) * align
+        self._ensure_rope(cap)
+        if B != self.B or cap > self.CAP:
+            torch.cuda.synchronize()
+            self.graphs = {}
+            self.k_cache = self.v_cache = None
+            torch.cuda.empty_cache()
+            dev = self.device
+            shape = (B, self.Nkv, cap, self.D)
+            self.k_cache = [torch.zeros(shape, dtype=BF16, device=dev) for _ in range(self.L)]
+            self.v_cache = [torch.zeros(shape, dtype=BF16, device=dev) for _ in range(self.L)]
+            self.hist_buf = torch.zeros((B, cap), dtype=torch.int64, device=dev)
+            self.pos_buf = torch.zeros((B,), dtype=torch.int32, device=dev)
+            self.s_buf = torch.zeros((1,), dtype=torch.int64, device=dev)
+            self.ntarget_buf = torch.full((1,), 1 << 40, dtype=torch.int64, device=dev)
+            self.B, self.CAP = B, cap
+            self.bufs = {}
+            ring = CONFIG["pipeline_depth"] + 2
+            self.pin_nxt = [torch.zeros((B,), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
+            self.events = [torch.cuda.Event() for _ in range(ring)]
+            _log(f"state B={B} CAP={cap} kv={2 * self.L * B * self.Nkv * cap * self.D * 2 / 2**30:.2f}GiB")
+        if CONFIG["graphs"] and 1 not in self.graphs:
+            self._capture(1)
+
+    def _buffers(self, B, T):
+        """Static activation buffers for a (B, T) step, reused by every replay."""
+        key = (B, T)
+        if key not in self.bufs:
+            M, dev = B * T, self.device
+            S = ops.choose_num_splits(B, self.Nkv, self.CAP)
+            lm_cfg = ops.lm_head_config(M, self.V, self.H)
+            self.bufs[key] = {
+                "h": torch.empty((M, self.H), dtype=BF16, device=dev),
+                "qkv": torch.empty((M, (self.Nq + 2 * self.Nkv) * self.D), dtype=BF16, device=dev),
+                "q": torch.empty((B, T, self.Nq, self.D), dtype=BF16, device=dev),
+                "a": torch.empty((B, T, self.Nq * self.D), dtype=BF16, device=dev),
+                "p": torch.empty((M, self.I), dtype=BF16, device=dev),
+                "next": torch.empty((M,), dtype=torch.int64, device=dev),
+                "splits": S,
+                "attn_ws": torch.empty(max(4, ops.attn_workspace_bytes(B, T, self.Nq, self.Nkv, self.D, S)),
+                                       dtype=torch.uint8, device=dev),
+                "lm_cfg": lm_cfg,
+                "lm_ws": torch.empty(ops.argmax_workspace_bytes(M, self.V, lm_cfg[0]), dtype=torch.uint8,
+                                     device=dev),
+            }
+        return self.bufs[key]
+
+    # ------------------------------------------------------------------ decode step
+    def _step(self, T, tok=None, hidden=None):
+        """One decode step of ``T`` tokens per sequence (``engine/engine.py:1093-1121``).
+
+        Token ids come from ``hist[b, pos[b]]`` (T = 1, the plain step) or from
+        ``tok [B, T]`` int64. Positions are ``pos_buf``; K/V are written at
+        ``pos + t``. Returns the greedy ``next [B*T]`` int64 buffer. Issues only
+        HIP kernels and allocates nothing, so it is capturable.
+        """
+        B = self.B
+        M = B * T
+        b = self._buffers(B, T)
+        h, qkv, q, a, p = b["h"], b["qkv"], b["q"], b["a"], b["p"]
+        stream = torch.cuda.current_stream().cuda_stream
+        if tok is None:
+            assert T == 1
+            ops._lib.call("qwen_embed", None, self.hist_buf.data_ptr(), self.pos_buf.data_ptr(), self.CAP,
+                          self.embed.data.data_ptr(), h.data_ptr(), M, self.V, self.H, stream)
+        else:
+            ops.embed(tok.reshape(-1), self.embed, out=h)
+        for l, w in enumerate(self.layers):
+            ops.fused_linear(h, w.w_qkv, norm_w=w.ln1, eps=self.eps, out=qkv)
+            ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
+                                   self.k_cache[l], self.v_cache[l], out=q)
+            ops.attn_decode(q, self.k_cache[l], self.v_cache[l], self.pos_buf, self.scale, b["splits"], len_add=T,
+                            out=a, workspace=b["attn_ws"])
+            ops.fused_linear(a.view(M, -1), w.w_o, residual=h, out=h)
+            ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p)
+            ops.fused_linear(p, w.w_down, residual=h, out=h)
+            if hidden is not None:
+                hidden.append(h.clone())
+        ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"], out=b["next"],
+                           workspace=b["lm_ws"])
+        return b["next"]
+
+    def _plain_step(self):
+        """``_plain_step`` (``engine/engine.py:941-953``): read hist[pos], step, write hist[pos+1], pos += 1."""
+        nxt = self._step(1)
+        ops._lib.call("qwen_plain_update", nxt.data_ptr(), self.hist_buf.data_ptr(), self.pos_buf.data_ptr(),
+                      self.s_buf.data_ptr(), self.ntarget_buf.data_ptr(), self.B, self.CAP,
+                      torch.cuda.current_stream().cuda_stream)
+        return nxt
+
+    def verify_step(self, tok: torch.Tensor) -> torch.Tensor:
+        """Greedy next token at every position of ``tok [B, T]`` fed at ``pos_buf`` (the speculative
+        verify forward of ``engine/engine.py:979-993``); writes K/V for those T slots, does not
+        advance the positions. Returns ``[B, T]`` int64."""
+        B, T = tok.shape
+        assert B == self.B and B * T <= 32 and T <= 16
+        return self._step(T, tok=tok.to(self.device, torch.int64).contiguous()).view(B, T)
+
+    def _capture(self, T):
+        """Record one plain decode step into a HIP graph (``engine/engine.py:1005-1042``)."""
+        assert T == 1
+        pos_saved = self.pos_buf.clone()
+        hist_saved = self.hist_buf.clone()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            self.pos_buf.fill_(1)
+            self._plain_step()              # warm-up (allocates nothing new)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        self.pos_buf.fill_(1)
+        with torch.cuda.graph(graph):
+            out = self._plain_step()
+        torch.cuda.synchronize()
+        self.graphs[T] = (graph, out)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.pos_buf.fill_(1)
+        start.record()
+        for _ in range(5):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        self.step_ms[T] = start.elapsed_time(end) / 5
+        # Capture wrote K/V at slot 1 and hist[:, 2]: the prompt forward and the
+        # first decode steps overwrite those slots before anything reads them.
+        self.pos_buf.copy_(pos_saved)
+        self.hist_buf.copy_(hist_saved)
+        torch.cuda.synchronize()
+        _log(f"captured T={T} graph; replay {self.step_ms[T]:.3f} ms/step")
+
+    # ------------------------------------------------------------------ prompt forward
+    def _prefill_attention(self, q, kc, vc, S):
+        """Causal attention of the prompt: q ``[Bs, S, Nq, D]``, cache views -> ``[Bs*S, Nq*D]``.
+
+        Uses torch SDPA restricted to its flash / memory-efficient kernels; if
+        neither accepts the shape, the decode-attention kernel runs over
+        16-token chunks of the prompt (same causal rule).
+        """
+        Bs = q.shape[0]
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        if self.sdpa_mode != "chunked":
+            try:
+                qt = q.transpose(1, 2)
+                rep = self.Nq // self.Nkv
+                k = kc[:, :, :S]
+                v = vc[:, :, :S]
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    if self.sdpa_mode in (None, "gqa"):
+                        try:
+                            out = F.scaled_dot_product_attention(qt, k, v, is_causal=True, scale=self.scale,
+                                                                 enable_gqa=True)
+                            self.sdpa_mode = "gqa"
+                            return out.transpose(1, 2).reshape(Bs * S, self.Nq * self.D)
+                        except RuntimeError:
+                            self.sdpa_mode = "expand"
+                    ke = k[:, :, None].expand(Bs, self.Nkv, rep, S, self.D).reshape(Bs, self.Nq, S, self.D)
+                    ve = v[:, :, None].expand(Bs, self.Nkv, rep, S, self.D).reshape(Bs, self.Nq, S, self.D)
+                    out = F.scaled_dot_product_attention(qt, ke, ve, is_causal=True, scale=self.scale)
+                    return out.transpose(1, 2).reshape(Bs * S, self.Nq * self.D)
+            except RuntimeError as error:
+                _log(f"SDPA flash/efficient unavailable ({error!r}); chunked decode-attention kernel")
+                self.sdpa_mode = "chunked"
+        out = torch.empty((Bs, S, self.Nq * self.D), dtype=BF16, device=self.device)
+        lengths = torch.empty((Bs,), dtype=torch.int32, device=self.device)
+        for t0 in range(0, S, 16):
+            T = min(16, S - t0)
+            lengths.fill_(t0 + T)
+            splits = ops.choose_num_splits(Bs, self.Nkv, t0 + T)
+            out[:, t0:t0 + T] = ops.attn_decode(q[:, t0:t0 + T].contiguous(), kc, vc, lengths, self.scale, splits)
+        return out.reshape(Bs * S, self.Nq * self.D)
+
+    def _prefill(self, ids):
+        """Prompt forward (``engine/engine.py:1181-1189``): batch slices of at most prefill_rows rows."""
+        B, S = ids.shape
+        rows_per = max(1, CONFIG["prefill_rows"] // S)
+        firsts = []
+        for b0 in range(0, B, rows_per):
+            b1 = min(B, b0 + rows_per)
+            firsts.append(self._prefill_slice(ids[b0:b1], b0))
+        return firsts[0] if len(firsts) == 1 else torch.cat(firsts)
+
+    def _prefill_slice(self, ids, b0, hidden=None):
+        """``_prefill_slice`` (``engine/engine.py:1191-1221``) for rows ``b0 .. b0 + Bs``."""
+        Bs, S = ids.shape
+        b1 = b0 + Bs
+        pos = torch.zeros((Bs,), dtype=torch.int32, device=self.device)
+        h = ops.embed(ids.reshape(-1).contiguous(), self.embed)
+        d = None
+        for l, w in enumerate(self.layers):
+            kc = self.k_cache[l][b0:b1]
+            vc = self.v_cache[l][b0:b1]
+            if d is None:
+                n = ops.rms_norm(h, w.ln1, self.eps)
+            else:
+                h, n = ops.add_rms_norm(h, d, w.ln1, self.eps)
+            qkv = F.linear(n, w.r_qkv)
+            q = ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, pos, S, kc, vc)
+            a = self._prefill_attention(q, kc, vc, S)
+            o = F.linear(a, w.r_o)
+            h, n = ops.add_rms_norm(h, o, w.ln2, self.eps)
+            d = F.linear(ops.silu_mul(F.linear(n, w.r_gu)), w.r_down)
+            if hidden is not None:
+                hidden.append(ops.add_rms_norm(h, d, w.ln1, self.eps)[0])
+        last = torch.arange(Bs, device=self.device) * S + (S - 1)
+        hl, _ = ops.add_rms_norm(h.index_select(0, last), d.index_select(0, last), self.final_norm, self.eps)
+        firsts = []
+        for r0 in range(0, Bs, 32):
+            firsts.append(ops.lm_head_argmax(hl[r0:r0 + 32].contiguous(), self.final_norm, self.eps, self.embed))
+        return firsts[0] if len(firsts) == 1 else torch.cat(firsts)
+
+    # ------------------------------------------------------------------ generate
+    def generate(self, input_ids: list[list[int]], max_new_tokens: int):
+        """Greedy continuation of every sequence, one step at a time (``engine/engine.py:1225-1250``).
+
+        Yields a list with one token id per sequence for each output step,
+        exactly ``max_new_tokens`` times. Never stops at end-of-sequence tokens.
+        """
+        B, S = len(input_ids), len(input_ids[0])
+        N = int(max_new_tokens)
+        if N <= 0:
+            return
+        if any(len(row) != S for row in input_ids):
+            raise ValueError("all prompts must have the same length")
+        ids_cpu = torch.tensor(input_ids, dtype=torch.int64)
+        if ids_cpu.numel() and (int(ids_cpu.min()) < 0 or int(ids_cpu.max()) >= self.V):
+            raise ValueError(f"token ids must lie in [0, {self.V})")
+        with torch.inference_mode():
+            self._prepare(B, S, N)
+            ids = ids_cpu.to(self.device)
+            first = self._prefill(ids)
+            self.hist_buf[:, :S].copy_(ids)
+            self.hist_buf[:, S].copy_(first)
+            self.pos_buf.fill_(S)
+            self.s_buf.fill_(S)
+            self.ntarget_buf.fill_(N)
+            yield from self._decode_loop(first, B, N)
+
+    def _decode_loop(self, first, B, N):
+        """Pipelined graph replays with async D2H copies into a pinned ring (``engine/engine.py:1254-1378``).
+
+        At most ``pipeline_depth + 1`` steps are in flight, and exactly N - 1
+        decode steps are launched (never one more than needed).
+        """
+        depth = CONFIG["pipeline_depth"]
+        ring = len(self.pin_nxt)
+        stream = torch.cuda.current_stream()
+        graph_out = self.graphs.get(1)
+
+        def launch(slot, mode):
+            if mode == "first":
+                self.pin_nxt[slot].copy_(first, non_blocking=True)
+            else:
+                if graph_out is not None:
+                    graph_out[0].replay()
+                    out = graph_out[1]
+                else:
+                    out = self._plain_step()
+                self.decode_launches += 1
+                self.pin_nxt[slot].copy_(out, non_blocking=True)
+            self.events[slot].record(stream)
+
+        inflight = deque()
+        launch(0, "first")
+        inflight.append(0)
+        launched = 1
+        yielded = 0
+        while yielded < N:
+            while len(inflight) <= depth and launched < N:
+                slot = launched % ring
+                launch(slot, "plain")
+                inflight.append(slot)
+                launched += 1
+            slot = inflight.popleft()
+            self.events[slot].synchronize()
+            yield [int(t) for t in self.pin_nxt[slot].tolist()]
+            yielded += 1

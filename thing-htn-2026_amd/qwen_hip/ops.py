@@ -1,0 +1,288 @@
+"""Operator wrappers over libqwen_hip.so, mirroring the reference's operator boundary.
+
+Names, argument order and meaning follow ``engine/engine.py:257-263`` (the
+``self.ops`` table) and the Triton wrappers they dispatch to
+(``engine/kernels/rmsnorm.py:141-207``, ``rope.py:169-226``,
+``attention.py:278-348``, ``silu.py:95-125``, ``gemm_fused.py:136-173``).
+Like the reference, each op allocates and returns its output (``torch.empty``,
+so under graph capture it comes from the graph's private pool), mutates only
+the caches it is documented to write, asserts its shape/dtype preconditions
+and raises ``RuntimeError`` if the native library is missing or a launch fails.
+All tensors must be on the GPU: there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+EPI_STORE, EPI_RES, EPI_SWIGLU = 0, 1, 2
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _gpu(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("qwen_hip ops run on the GPU only; got a tensor on " + str(t.device))
+
+
+def _nullable(t):
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------- norms
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """``Qwen3RMSNorm`` over the last dim (``rmsnorm.py:141-167``)."""
+    _gpu(x, w)
+    assert x.dtype == BF16 and w.dtype == BF16, "rms_norm expects bf16"
+    N = x.shape[-1]
+    assert w.numel() == N and w.is_contiguous()
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    _lib.call("qwen_rms_norm", x.data_ptr(), w.data_ptr(), y.data_ptr(), x.numel() // N, N, float(eps), _stream())
+    return y
+
+
+def add_rms_norm(x: torch.Tensor, r: torch.Tensor, w: torch.Tensor, eps: float):
+    """``h = bf16(x + r)``, ``y = rms_norm(h)``; returns ``(h, y)`` (``rmsnorm.py:170-207``)."""
+    _gpu(x, r, w)
+    assert x.dtype == BF16 and r.dtype == BF16 and w.dtype == BF16, "add_rms_norm expects bf16"
+    assert x.shape == r.shape, "add_rms_norm: x and r shapes differ"
+    N = x.shape[-1]
+    assert w.numel() == N and w.is_contiguous()
+    x, r = x.contiguous(), r.contiguous()
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    _lib.call("qwen_add_rms_norm", x.data_ptr(), r.data_ptr(), w.data_ptr(), h.data_ptr(), y.data_ptr(),
+              x.numel() // N, N, float(eps), _stream())
+    return h, y
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """``bf16(bf16(silu(gate)) * up)`` for ``gu [..., 2I]`` (``silu.py:95-125``)."""
+    _gpu(gu)
+    assert gu.dtype == BF16 and gu.shape[-1] % 2 == 0, "silu_mul expects bf16 [..., 2I]"
+    gu = gu.contiguous()
+    inter = gu.shape[-1] // 2
+    out = torch.empty((*gu.shape[:-1], inter), dtype=BF16, device=gu.device)
+    _lib.call("qwen_silu_mul", gu.data_ptr(), out.data_ptr(), gu.numel() // gu.shape[-1], inter, _stream())
+    return out
+
+
+# ------------------------------------------------------------ rope + cache
+
+def qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, T, k_cache, v_cache,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k RMSNorm + RoPE, K/V cache write; returns q ``[B, T, Nq, D]`` (``rope.py:169-226``)."""
+    _gpu(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache)
+    B, Nkv, CAP, D = k_cache.shape
+    M, W = qkv.shape
+    assert D == 128, f"head_dim must be 128, got {D}"
+    assert W % D == 0 and W // D > 2 * Nkv, f"qkv width {W} does not hold Nq + 2*{Nkv} heads of {D}"
+    Nq = W // D - 2 * Nkv
+    assert M == B * T, f"qkv has {M} rows but B*T = {B}*{T}"
+    assert qkv.dtype == BF16 and qkv.is_contiguous()
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and v_cache.shape == k_cache.shape
+    assert k_cache.dtype == BF16 and v_cache.dtype == BF16
+    assert q_norm_w.numel() == D and k_norm_w.numel() == D
+    assert cos_tab.dim() == 2 and cos_tab.shape[1] == D and cos_tab.is_contiguous() and sin_tab.shape == cos_tab.shape
+    assert cos_tab.dtype == BF16 and sin_tab.dtype == BF16
+    assert positions.dtype == torch.int32 and positions.numel() == B and positions.is_contiguous()
+    q = out if out is not None else torch.empty((B, T, Nq, D), dtype=BF16, device=qkv.device)
+    _lib.call("qwen_qk_norm_rope_cache", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+              cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
+              v_cache.data_ptr(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0], float(eps), _stream())
+    return q
+
+
+# --------------------------------------------------------------- attention
+
+def choose_num_splits(B: int, Nkv: int, cap: int) -> int:
+    """Context splits per (sequence, KV head) for a decode shape.
+
+    Targets about 2048 workgroups (8 per CU on 256 CUs) while keeping at least
+    64 cache slots per split; power of two in [1, 64]. Fixed per captured graph,
+    as in the reference (``attention.py:94-110``), where the target was 264.
+    """
+    want = max(1, math.ceil(2048 / max(1, B * Nkv)))
+    limit = max(1, cap // 64)
+    s = 1
+    while s * 2 <= min(want, limit, 64):
+        s *= 2
+    return s
+
+
+def attn_workspace_bytes(B, T, Nq, Nkv, D, num_splits) -> int:
+    return _lib.query("qwen_attn_workspace_bytes", B, T, Nq, Nkv, D, num_splits)
+
+
+def attn_decode(q, k_cache, v_cache, lengths, scale, num_splits, *, len_add: int = 0,
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal decode attention of ``T`` new queries over the cache (``attention.py:278-348``).
+
+    ``lengths [B]`` int32 counts valid slots including the ``T`` new ones
+    (plus ``len_add``); returns ``[B, T, Nq * D]`` bf16.
+    """
+    _gpu(q, k_cache, v_cache, lengths)
+    B, T, Nq, D = q.shape
+    Bk, Nkv, CAP, Dk = k_cache.shape
+    assert Bk == B and Dk == D and v_cache.shape == k_cache.shape, "q / cache shape mismatch"
+    assert q.dtype == BF16 and k_cache.dtype == BF16 and v_cache.dtype == BF16
+    assert k_cache.is_contiguous() and v_cache.is_contiguous(), "KV cache must be contiguous"
+    assert lengths.dtype == torch.int32 and lengths.numel() == B and lengths.is_contiguous()
+    assert Nq == 4 * Nkv and D == 128 and 1 <= T <= 16, "kernel supports G = 4, D = 128, T <= 16"
+    S = int(num_splits)
+    assert S >= 1
+    q = q.contiguous()
+    need = attn_workspace_bytes(B, T, Nq, Nkv, D, S)
+    if workspace is None:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    o = out if out is not None else torch.empty((B, T, Nq * D), dtype=BF16, device=q.device)
+    _lib.call("qwen_attn_decode", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), lengths.data_ptr(),
+              int(len_add), o.data_ptr(), workspace.data_ptr(), workspace.numel(), B, T, Nq, Nkv, D, CAP,
+              float(scale), S, _stream())
+    return o
+
+
+# ------------------------------------------------------- weights + GEMMs
+
+class TiledWeight:
+    """A projection weight ``[N, K]`` stored in MFMA-B tiles (see ``include/qwen_hip.h``).
+
+    ``pair`` marks a gate|up weight whose 16-row tiles are interleaved
+    (gate tile p, up tile p) for the SwiGLU epilogue.
+    """
+
+    __slots__ = ("data", "N", "K", "pair")
+
+    def __init__(self, data: torch.Tensor, N: int, K: int, pair: bool = False):
+        assert data.dtype == BF16 and data.numel() == N * K and data.is_contiguous()
+        assert N % 16 == 0 and K % 32 == 0
+        self.data, self.N, self.K, self.pair = data, int(N), int(K), bool(pair)
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel() * 2
+
+    @classmethod
+    def empty(cls, N: int, K: int, device, pair: bool = False):
+        return cls(torch.empty(N * K, dtype=BF16, device=device), N, K, pair)
+
+    @classmethod
+    def random(cls, N, K, seg_start, seg_tid, seed, scale, device, pair=False):
+        """Fill from the counter-based generator (``qwen_init_weight``)."""
+        t = cls.empty(N, K, device, pair)
+        init_weight(t.data, N, K, True, pair, seg_start, seg_tid, seed, scale)
+        return t
+
+
+def init_weight(dst: torch.Tensor, N, K, tiled, pair, seg_start, seg_tid, seed, scale) -> None:
+    _gpu(dst)
+    n = len(seg_start)
+    assert n == len(seg_tid) and 1 <= n <= 4
+    starts = (ctypes.c_int * n)(*[int(v) for v in seg_start])
+    tids = (ctypes.c_int * n)(*[int(v) for v in seg_tid])
+    _lib.call("qwen_init_weight", dst.data_ptr(), int(N), int(K), int(bool(tiled)), int(bool(pair)), starts, tids,
+              n, int(seed), float(scale), _stream())
+
+
+def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
+    """Re-lay a row-major ``[N, K]`` bf16 weight into MFMA-B tiles."""
+    _gpu(w)
+    assert w.dtype == BF16 and w.dim() == 2
+    w = w.contiguous()
+    N, K = w.shape
+    t = TiledWeight.empty(N, K, w.device, pair)
+    _lib.call("qwen_tile_weight", w.data_ptr(), t.data.data_ptr(), N, K, int(pair), _stream())
+    return t
+
+
+def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, int]:
+    """(ntw, ksplit) launch shape: enough wavefronts to cover 256 CUs (about 2048),
+    at least 8 k-steps (8 KB of weight per n-tile) per wavefront."""
+    ntw = 2 if silu_pair else 1
+    units = N // (16 * ntw)
+    KT = K // 32
+    ks = 1
+    while ks < 16 and units * ks < 2048 and KT // (ks * 2) >= 8:
+        ks *= 2
+    if (ntw == 2 or M > 16) and ks > 8:   # 16-wavefront variants exist for one n-tile, one m-tile
+        ks = 8
+    return ntw, ks
+
+
+def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps: float = 0.0, residual=None,
+                 silu_pair: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x @ w.T`` with optional RMSNorm prologue and residual / SwiGLU epilogue (``gemm_fused.py:136-173``).
+
+    ``x [M <= 32, K]`` bf16; ``w`` tiled ``[N, K]`` (for ``silu_pair`` a pair-
+    interleaved ``cat(gate, up)`` and the output is ``[M, N/2]``); ``norm_w [K]``;
+    ``residual [M, N]`` (may be the same tensor as ``out``). ``cfg`` is
+    ``(ntw, ksplit)`` or ``None`` for ``gemm_config``.
+    """
+    _gpu(x, norm_w, residual, out)
+    assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
+    M, K = x.shape
+    assert K == w.K and 1 <= M <= 32, f"x [{M}, {K}] vs weight K={w.K}; M must be in [1, 32]"
+    assert not (silu_pair and residual is not None)
+    assert silu_pair == w.pair, "silu_pair requires a pair-interleaved weight (and only then)"
+    if norm_w is not None:
+        assert norm_w.dtype == BF16 and norm_w.numel() == K and norm_w.is_contiguous()
+    ncols = w.N // 2 if silu_pair else w.N
+    if residual is not None:
+        assert residual.shape == (M, ncols) and residual.dtype == BF16 and residual.is_contiguous()
+    if out is None:
+        out = torch.empty((M, ncols), dtype=BF16, device=x.device)
+    assert out.shape == (M, ncols) and out.is_contiguous()
+    ntw, ks = cfg if cfg is not None else gemm_config(M, w.N, K, silu_pair)
+    epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
+    _lib.call("qwen_linear", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols, _nullable(norm_w),
+              float(eps), _nullable(residual), epi, ntw, ks, _stream())
+    return out
+
+
+def lm_head_config(M: int, N: int, K: int) -> tuple[int, int]:
+    return 2, 2
+
+
+def argmax_workspace_bytes(M, N, ntw) -> int:
+    return _lib.query("qwen_argmax_workspace_bytes", M, N, ntw)
+
+
+def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWeight, *, cfg=None,
+                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Final RMSNorm + tied LM head + first-index argmax over bf16 logits -> int64 ``[M]``."""
+    _gpu(x, norm_w, out, workspace)
+    assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
+    M, K = x.shape
+    assert K == w.K and 1 <= M <= 32 and not w.pair
+    ntw, ks = cfg if cfg is not None else lm_head_config(M, w.N, K)
+    need = argmax_workspace_bytes(M, w.N, ntw)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty((M,), dtype=torch.int64, device=x.device)
+    _lib.call("qwen_lm_head_argmax", x.data_ptr(), norm_w.data_ptr(), float(eps), w.data.data_ptr(), M, w.N, K,
+              workspace.data_ptr(), workspace.numel(), out.data_ptr(), ntw, ks, _stream())
+    return out
+
+
+def embed(tok: torch.Tensor, w: TiledWeight, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.embedding(tok, W)`` from the tiled tied table; ``tok`` int64 ``[M]``."""
+    _gpu(tok)
+    assert tok.dtype == torch.int64 and tok.is_contiguous()
+    M = tok.numel()
+    if out is None:
+        out = torch.empty((M, w.K), dtype=BF16, device=tok.device)
+    _lib.call("qwen_embed", tok.data_ptr(), None, None, 0, w.data.data_ptr(), out.data_ptr(), M, w.N, w.K,
+              _stream())
+    return out
