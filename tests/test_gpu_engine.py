@@ -107,8 +107,7 @@ def test_verify_step_matches_plain_steps(small):
     g = torch.Generator().manual_seed(2)
     drafts = torch.randint(0, V, (B, T - 1), generator=g)
     tok = torch.cat([torch.tensor(tokens), drafts], 1)           # [B, T]: accepted token + 4 drafts
-    eng.pos_buf.fill_(S)
-    got = eng.verify_step(tok).cpu()
+    got = eng.verify_step(tok, [S] * B).cpu()
     ref.prepare(B, eng.CAP)
     ref.prefill(torch.tensor(prompt))
     pos = torch.full((B,), S, dtype=torch.int32)
@@ -133,11 +132,8 @@ def test_qwen4b_shapes_hidden_states(qwen4b_two_layers):
     B, S = 2, 24
     prompt = _prompt(B, S, cfg["vocab_size"], 5)
     _run(eng, prompt, 1, cfg["vocab_size"])           # prefill + state
-    hidden = []
     tok = torch.tensor(prompt)[:, -1:]
-    eng.pos_buf.fill_(S - 1)                            # re-run the last prompt token as a decode step
-    with torch.inference_mode():
-        eng._step(1, tok=tok.to(eng.device), hidden=hidden)
+    hidden = eng.step_hidden(tok, [S - 1] * B)          # re-run the last prompt token as a decode step
     ref.prepare(B, eng.CAP)
     ref.prefill(torch.tensor(prompt)[:, :S - 1])
     want = []

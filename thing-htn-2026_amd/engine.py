@@ -320,13 +320,26 @@ class Engine:
                       torch.cuda.current_stream().cuda_stream)
         return nxt
 
-    def verify_step(self, tok: torch.Tensor) -> torch.Tensor:
-        """Greedy next token at every position of ``tok [B, T]`` fed at ``pos_buf`` (the speculative
-        verify forward of ``engine/engine.py:979-993``); writes K/V for those T slots, does not
-        advance the positions. Returns ``[B, T]`` int64."""
+    def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
+        """Greedy next token at every position of ``tok [B, T]`` (the speculative verify forward
+        of ``engine/engine.py:979-993``): token ``t`` of row ``b`` sits at ``positions[b] + t``;
+        K/V are written for those slots. Returns ``[B, T]`` int64 (host sync)."""
         B, T = tok.shape
-        assert B == self.B and B * T <= 32 and T <= 16
-        return self._step(T, tok=tok.to(self.device, torch.int64).contiguous()).view(B, T)
+        assert B == self.B and B * T <= 32 and T <= 16, "verify needs the prepared batch, B*T <= 32, T <= 16"
+        with torch.inference_mode():
+            pos = torch.as_tensor(positions, dtype=torch.int32).reshape(B)
+            self.pos_buf.copy_(pos.to(self.device))
+            out = self._step(T, tok=tok.to(self.device, torch.int64).contiguous()).view(B, T).clone()
+        return out
+
+    def step_hidden(self, tok: torch.Tensor, positions) -> list:
+        """One eager decode step of ``tok [B, 1]`` at ``positions``; returns the residual stream
+        after every layer (for per-layer parity checks)."""
+        hidden = []
+        with torch.inference_mode():
+            self.pos_buf.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
+            self._step(1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
+        return [h.clone() for h in hidden]
 
     def _capture(self, T):
         """Record one plain decode step into a HIP graph (``engine/engine.py:1005-1042``)."""
