@@ -77,17 +77,18 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3):
     from qwen_hip import ops
     B = eng.B
     b = eng._buffers(B, 1)
-    h, p = b["h"], b["p"]
+    h, p, psq, cfg = b["h"], b["p"], b["psq"], b["cfg_gu"]
     stream = torch.cuda.current_stream()
+    ops.sumsq16(h, out=psq)
     for w in eng.layers[:2]:
-        ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p)
+        ops.fused_linear(h, w.w_gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     n = 0
     for _ in range(reps_per_layer):
         for w in eng.layers:
-            ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p)
+            ops.fused_linear(h, w.w_gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq)
             n += 1
     end.record(stream)
     end.synchronize()
@@ -113,7 +114,8 @@ def cpu_baseline(eng, cfg, B, S, layers):
     ref = CpuQwen3(dict(cfg, num_hidden_layers=layers), weights)
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    ref.prepare(B, ((S + 64 + 63) // 64) * 64)
+    max_steps = 64
+    ref.prepare(B, ((S + max_steps + 64) // 64) * 64)
     g = torch.Generator().manual_seed(1)
     ids = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
     with torch.inference_mode():
@@ -123,7 +125,7 @@ def cpu_baseline(eng, cfg, B, S, layers):
         ref.plain_step()                       # warm-up
         t_layers, t_head, steps = 0.0, 0.0, 0
         t_end = time.perf_counter() + 15.0
-        while time.perf_counter() < t_end or steps < 2:
+        while (time.perf_counter() < t_end or steps < 2) and steps < max_steps:
             tok = ref.hist.gather(1, ref.pos.to(torch.int64)[:, None])
             t0 = time.perf_counter()
             h = ref.w["embed"][tok.reshape(-1)]

@@ -62,31 +62,42 @@ int qwen_attn_decode(const void* q, const void* k_cache, const void* v_cache, co
                      void* out, void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
                      int CAP, float scale, int num_splits, hipStream_t stream);
 
-/* out = x @ W^T with optional RMSNorm prologue (norm_w != NULL) and epilogue
- * epi = 0 store, 1 residual add (out = bf16(residual + bf16(acc)); residual may alias out),
+/* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
+ * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed
+ * projections consume (psq_in below). No reference counterpart: it is the first
+ * half of the reference's RMSNorm (rmsnorm.py:91-93) split out so that producers
+ * can emit it. */
+int qwen_sumsq16(const void* x, float* psq, int M, int K, hipStream_t stream);
+
+/* out = x @ W^T with optional RMSNorm prologue (norm_w != NULL; psq_in = x's
+ * qwen_sumsq16 partials [M, K/16]) and epilogue
+ * epi = 0 store, 1 residual add (out = bf16(residual + bf16(acc)); residual may alias out;
+ * psq_out != NULL also writes the new rows' [M, N/16] partials),
  * 2 SwiGLU pair (W tiled with pair interleave; N = 2I rows; out has I columns).
  * x: [M, K] (M <= 32), W tiled [N, K]. ntw (1|2) n-tiles and ksplit (1|2|4|8|16)
  * wavefronts per workgroup select the launch shape.
  * Replaces the projections of engine/engine.py:1108-1118 (_mm / F.linear) and
  * engine/kernels/gemm_fused.py:136-173 (fused_linear). */
 int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* norm_w,
-                float eps, const void* residual, int epi, int ntw, int ksplit, hipStream_t stream);
+                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int ksplit,
+                hipStream_t stream);
 
 /* Workspace bytes for qwen_lm_head_argmax. */
 long long qwen_argmax_workspace_bytes(int M, int N, int ntw);
 
 /* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
- * out_tok[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]).
+ * out_tok[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.
  * Replaces engine/engine.py:1119-1121 (final add_rms_norm, lm_head _mm, argmax). */
-int qwen_lm_head_argmax(const void* x, const void* norm_w, float eps, const void* w_tiled, int M, int N, int K,
-                        void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw, int ksplit,
-                        hipStream_t stream);
+int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, float eps, const void* w_tiled, int M,
+                        int N, int K, void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw,
+                        int ksplit, hipStream_t stream);
 
 /* Embedding gather from the tiled tied table: out[m] = W[tok[m]], or, with tok == NULL,
  * out[m] = W[hist[m, pos[m]]] (the decode step's token read, engine/engine.py:941-946).
+ * psq_out != NULL also writes the rows' qwen_sumsq16 partials. Ids are clamped to [0, V).
  * Replaces F.embedding at engine/engine.py:1101. */
 int qwen_embed(const int64_t* tok, const int64_t* hist, const int32_t* pos, int cap, const void* w_tiled, void* out,
-               int M, long long V, int K, hipStream_t stream);
+               float* psq_out, int M, long long V, int K, hipStream_t stream);
 
 /* Token bookkeeping after a plain decode step: hist[b, pos[b]+1] = next[b], pos[b] += 1,
  * frozen rows ((pos+1 - s_buf) >= ntarget) write slot cap-1 and keep pos.

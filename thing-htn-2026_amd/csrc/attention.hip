@@ -7,8 +7,8 @@
 // PV product; fp32 row sums; LSE merge across splits; one final bf16 rounding.
 //
 // Work decomposition (CDNA4, 64-wide wavefronts):
-//   grid (B*Nkv, S), one workgroup per (sequence, KV head, context split),
-//   one wavefront per new query token t, G = 4 query heads per wavefront.
+//   grid (B*Nkv, S, T): one single-wavefront workgroup per (sequence, KV head,
+//   context split, new query token t), G = 4 query heads per wavefront.
 //   Inside a wavefront, lane = 8*slot + c: 8 key slots x 8 lanes per key.
 //   Lane c of a slot owns dims [8c, 8c+8) and [64+8c, 64+8c+8), so one key
 //   row (256 B) is read by its 8 lanes as 16 B loads and the 8 keys of one
@@ -23,15 +23,16 @@ namespace {
 
 constexpr float NEG_BIG = -1e30f;
 constexpr int ATT_D = 128;
-constexpr int KEYS_PER_ITER = 32;  // 8 slots x 4 keys per slot per iteration
+constexpr int KU = 2;                     // keys per slot per iteration
+constexpr int KEYS_PER_ITER = 8 * KU;     // 8 slots
 
 template <int G>
-__global__ void __launch_bounds__(1024) attn_partial_kernel(
+__global__ void __launch_bounds__(64) attn_partial_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,
     const int32_t* __restrict__ lengths, int len_add, float* __restrict__ part_ml, float* __restrict__ part_acc, int T,
     int Nkv, int CAP, int S, float scale) {
-  const int lane = threadIdx.x & 63;
-  const int t = threadIdx.x >> 6;
+  const int lane = threadIdx.x;
+  const int t = blockIdx.z;
   const int slot = lane >> 3, c = lane & 7;
   const long long bh = blockIdx.x;
   const long long b = bh / Nkv;
@@ -67,11 +68,11 @@ __global__ void __launch_bounds__(1024) attn_partial_kernel(
   const bf16_t* vbase = v_cache + (bh * CAP) * ATT_D;
 
   for (int base = start; base < kend; base += KEYS_PER_ITER) {
-    uint4 kr[4][2], vr[4][2];
-    bool valid[4];
+    uint4 kr[KU][2], vr[KU][2];
+    bool valid[KU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int kk = base + u * 8 + slot;
+    for (int u = 0; u < KU; ++u) {
+      const int kk = base + u * 8 + slot;  // 8 consecutive keys per load instruction
       valid[u] = kk < kend;
       if (valid[u]) {
         const bf16_t* kp = kbase + (long long)kk * ATT_D;
@@ -84,9 +85,9 @@ __global__ void __launch_bounds__(1024) attn_partial_kernel(
         kr[u][0] = kr[u][1] = vr[u][0] = vr[u][1] = make_uint4(0, 0, 0, 0);
       }
     }
-    float s[4][G];
+    float s[KU][G];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < KU; ++u) {
       float kf[16];
       unpack8(kr[u][0], kf);
       unpack8(kr[u][1], kf + 8);
@@ -101,19 +102,21 @@ __global__ void __launch_bounds__(1024) attn_partial_kernel(
         s[u][g] = valid[u] ? d * scale : NEG_BIG;
       }
     }
-    float vf[4][16];
+    float vf[KU][16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < KU; ++u) {
       unpack8(vr[u][0], vf[u]);
       unpack8(vr[u][1], vf[u] + 8);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float mn = fmaxf(fmaxf(m[g], fmaxf(s[0][g], s[1][g])), fmaxf(s[2][g], s[3][g]));
-      const float alpha = __expf(m[g] - mn);
-      float p[4], psum = 0.f;
+      float mn = m[g];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < KU; ++u) mn = fmaxf(mn, s[u][g]);
+      const float alpha = __expf(m[g] - mn);
+      float p[KU], psum = 0.f;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
         p[u] = valid[u] ? __expf(s[u][g] - mn) : 0.f;
         psum += p[u];
       }
@@ -122,7 +125,7 @@ __global__ void __launch_bounds__(1024) attn_partial_kernel(
       for (int e = 0; e < 16; ++e) {
         float a = acc[g][e] * alpha;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a = fmaf(rbf(p[u]), vf[u][e], a);
+        for (int u = 0; u < KU; ++u) a = fmaf(rbf(p[u]), vf[u][e], a);
         acc[g][e] = a;
       }
       m[g] = mn;
@@ -220,7 +223,7 @@ int qwen_attn_decode(const void* q, const void* k_cache, const void* v_cache, co
   // acc rows first (512 B each, so every float4 store is aligned), then (m, l) pairs.
   float* part_acc = (float*)workspace;
   float* part_ml = part_acc + BH * num_splits * R * ATT_D;
-  attn_partial_kernel<4><<<dim3((unsigned)BH, num_splits), 64 * T, 0, stream>>>(
+  attn_partial_kernel<4><<<dim3((unsigned)BH, num_splits, T), 64, 0, stream>>>(
       (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, lengths, len_add, part_ml, part_acc, T, Nkv, CAP,
       num_splits, scale);
   hipError_t e = hipGetLastError();

@@ -40,6 +40,8 @@ struct GemmParams {
   bf16_t* out;        // [M, ld_out]
   float* pval;        // [units, M] argmax partial values (EPI_ARGMAX)
   int32_t* pidx;      // [units, M] argmax partial indices
+  const float* psq_in;  // [M, K/16] partial sums of squares of x per 16 columns (NORM)
+  float* psq_out;       // [M, N/16] same for the output rows (EPI_RES, may be null)
   int M, N, K, ld_out;
   float eps;
 };
@@ -56,9 +58,10 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
   const int k0 = min(KT, wave * kpw);
   const int k1 = min(KT, k0 + kpw);
 
-  __shared__ float ssq[NORM ? KSPLIT * MT * 16 : 1];
   __shared__ f32x4_t red[KSPLIT > 1 ? KSPLIT * MT * NTW * 64 : 1];
 
+  // Rows of the A operand this lane feeds: m = r + 16*mt. Rows past M read
+  // row 0 (always valid) and are zeroed, so the loads need no branch.
   const bf16_t* xrow[MT];
   bool mval[MT];
 #pragma unroll
@@ -68,29 +71,21 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
     xrow[mt] = p.x + (size_t)(mval[mt] ? m : 0) * p.K + 8 * q;
   }
 
+  // RMSNorm statistics: the producer of x left one partial sum of squares per
+  // 16 columns (rounded bf16 values, squared and summed in fp32). The four
+  // lanes of a row each add a quarter of them in a fixed order, so every
+  // workgroup derives bit-identical factors.
   float rinv[MT];
   if constexpr (NORM) {
+    const int nu = p.K >> 4;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      const float* ps = p.psq_in + (size_t)(mval[mt] ? r + 16 * mt : 0) * nu;
       float s = 0.f;
-      if (mval[mt]) {
-        for (int kt = k0; kt < k1; ++kt) {
-          float f[8];
-          unpack8(*reinterpret_cast<const uint4*>(xrow[mt] + kt * 32), f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
-        }
-      }
+      for (int u = q; u < nu; u += 4) s += ps[u];
       s += __shfl_xor(s, 16, 64);
       s += __shfl_xor(s, 32, 64);
-      if (q == 0) ssq[(wave * MT + mt) * 16 + r] = s;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float tot = 0.f;
-      for (int w = 0; w < KSPLIT; ++w) tot += ssq[(w * MT + mt) * 16 + r];
-      rinv[mt] = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+      rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
     }
   }
 
@@ -106,11 +101,12 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
   for (int nt = 0; nt < NTW; ++nt) wrow[nt] = (size_t)(unit * NTW + nt) * KT * 64 + lane;
   const uint4* nwp = reinterpret_cast<const uint4*>(p.nw);
 
-  auto make_a = [&](const uint4& raw, int kt, int mt) -> bf16x8_t {
+  auto make_a = [&](uint4 raw, const uint4& gain, int mt) -> bf16x8_t {
+    if (!mval[mt]) raw = make_uint4(0, 0, 0, 0);
     if constexpr (NORM) {
       float f[8], g[8], o[8];
       unpack8(raw, f);
-      unpack8(nwp[kt * 4 + q], g);
+      unpack8(gain, g);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = mul_rn(g[e], rbf(mul_rn(f[e], rinv[mt])));
       return as_bf16x8(pack8(o));
@@ -119,39 +115,36 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
     }
   };
 
-  int kt = k0;
-  for (; kt + U <= k1; kt += U) {
-    uint4 bt[U][NTW], at[U][MT];
+  // Each batch issues all of its loads first (weights from HBM, activations and
+  // gains from L2), then runs the MFMAs in arrival order. The last batch of a
+  // range is padded by re-reading step k1-1 (a cache hit) with a zero A
+  // operand, so there is no serial remainder loop.
+  for (int kt = k0; kt < k1; kt += U) {
+    uint4 bt[U][NTW], at[U][MT], gt[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int kk = min(kt + u, k1 - 1);
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) bt[u][nt] = wt[wrow[nt] + (size_t)(kt + u) * 64];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        at[u][mt] = mval[mt] ? *reinterpret_cast<const uint4*>(xrow[mt] + (kt + u) * 32) : make_uint4(0, 0, 0, 0);
+      for (int nt = 0; nt < NTW; ++nt) bt[u][nt] = wt[wrow[nt] + (size_t)kk * 64];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int kk = min(kt + u, k1 - 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) at[u][mt] = *reinterpret_cast<const uint4*>(xrow[mt] + kk * 32);
+      if constexpr (NORM) gt[u] = nwp[kk * 4 + q];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = kt + u < k1;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8_t a = make_a(at[u][mt], kt + u, mt);
+        bf16x8_t a = make_a(at[u][mt], gt[u], mt);
+        if (!live) a = as_bf16x8(make_uint4(0, 0, 0, 0));
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt)
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bt[u][nt]), acc[mt][nt], 0, 0, 0);
       }
-    }
-  }
-  for (; kt < k1; ++kt) {
-    uint4 bt[NTW];
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) bt[nt] = wt[wrow[nt] + (size_t)kt * 64];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint4 raw = mval[mt] ? *reinterpret_cast<const uint4*>(xrow[mt] + kt * 32) : make_uint4(0, 0, 0, 0);
-      const bf16x8_t a = make_a(raw, kt, mt);
-#pragma unroll
-      for (int nt = 0; nt < NTW; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bt[nt]), acc[mt][nt], 0, 0, 0);
     }
   }
 
@@ -198,22 +191,32 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
           p.pidx[(size_t)unit * p.M + m] = bidx;
         }
       } else {
-        if (m >= p.M) continue;
-        bf16_t* orow = p.out + (size_t)m * p.ld_out;
+        const bool mok = m < p.M;
+        bf16_t* orow = p.out + (size_t)(mok ? m : 0) * p.ld_out;
         if constexpr (EPI == EPI_SWIGLU) {
           const float g = rbf(acc[mt][0][i]);
           const float u = rbf(acc[mt][1][i]);
           const float s = rbf(g / (1.0f + expf(-g)));
-          orow[unit * 16 + r] = f2bf(mul_rn(s, u));
+          if (mok) orow[unit * 16 + r] = f2bf(mul_rn(s, u));
         } else {
 #pragma unroll
           for (int nt = 0; nt < NTW; ++nt) {
             const int col = (unit * NTW + nt) * 16 + r;
             if constexpr (EPI == EPI_RES) {
-              const float rv = bf2f(p.res[(size_t)m * p.ld_out + col]);
-              orow[col] = f2bf(add_rn(rv, rbf(acc[mt][nt][i])));
+              const float rv = mok ? bf2f(p.res[(size_t)m * p.ld_out + col]) : 0.f;
+              const bf16_t o = f2bf(add_rn(rv, rbf(acc[mt][nt][i])));
+              if (mok) orow[col] = o;
+              if (p.psq_out) {  // partial sum of squares of the new row over these 16 columns
+                const float v = bf2f(o);
+                float sq = mul_rn(v, v);
+                sq += __shfl_xor(sq, 1, 64);
+                sq += __shfl_xor(sq, 2, 64);
+                sq += __shfl_xor(sq, 4, 64);
+                sq += __shfl_xor(sq, 8, 64);
+                if (mok && r == 0) p.psq_out[(size_t)m * (p.N >> 4) + (col >> 4)] = sq;
+              }
             } else {
-              orow[col] = f2bf(acc[mt][nt][i]);
+              if (mok) orow[col] = f2bf(acc[mt][nt][i]);
             }
           }
         }
@@ -294,17 +297,20 @@ extern "C" {
 // epi: 0 = store, 1 = residual add (residual may alias out), 2 = SwiGLU pair
 // (N counts gate + up rows; out has N/2 columns). norm_w == nullptr: no norm prologue.
 int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* norm_w,
-                float eps, const void* residual, int epi, int ntw, int ksplit, hipStream_t stream) {
+                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int ksplit,
+                hipStream_t stream) {
   int st = check_common(x, w_tiled, M, N, K, ntw, ksplit);
   if (st) return st;
   if (!out) return QWEN_ENULL;
   if (epi == EPI_RES && !residual) return QWEN_ENULL;
+  if (norm_w && !psq_in) return QWEN_ENULL;
+  if (psq_out && (epi != EPI_RES || N % 16 != 0)) return QWEN_EARG;
   if (epi == EPI_SWIGLU && ntw != 2) return QWEN_EARG;
   if (epi < EPI_STORE || epi > EPI_SWIGLU) return QWEN_EARG;
   const int out_cols = epi == EPI_SWIGLU ? N / 2 : N;
   if (ld_out < out_cols) return QWEN_EARG;
   GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, (const bf16_t*)residual,
-               (bf16_t*)out, nullptr, nullptr, M, N, K, ld_out, eps};
+               (bf16_t*)out, nullptr, nullptr, psq_in, psq_out, M, N, K, ld_out, eps};
   const int units = N / (16 * ntw);
   const int mt = M > 16 ? 2 : 1;
   // Instantiated variants: norm+store (QKV), store (plain linear), residual
@@ -323,20 +329,20 @@ long long qwen_argmax_workspace_bytes(int M, int N, int ntw) {
 
 // Final RMSNorm (norm_w) + LM head GEMM + argmax over the bf16 logits,
 // lowest index on ties. out_tok: [M] int64.
-int qwen_lm_head_argmax(const void* x, const void* norm_w, float eps, const void* w_tiled, int M, int N, int K,
-                        void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw, int ksplit,
-                        hipStream_t stream) {
+int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, float eps, const void* w_tiled, int M,
+                        int N, int K, void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw,
+                        int ksplit, hipStream_t stream) {
   int st = check_common(x, w_tiled, M, N, K, ntw, ksplit);
   if (st) return st;
-  if (!out_tok || !workspace) return QWEN_ENULL;
+  if (!out_tok || !workspace || !norm_w || !psq_in) return QWEN_ENULL;
   if (workspace_bytes < qwen_argmax_workspace_bytes(M, N, ntw)) return QWEN_EWORKSPACE;
   const int units = N / (16 * ntw);
   float* pval = (float*)workspace;
   int32_t* pidx = (int32_t*)(pval + (size_t)units * M);
   GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, nullptr, nullptr, pval, pidx,
-               M, N, K, 0, eps};
+               psq_in, nullptr, M, N, K, 0, eps};
   const int mt = M > 16 ? 2 : 1;
-  st = norm_w ? dispatch<true, EPI_ARGMAX>(p, units, mt, ntw, ksplit, stream) : QWEN_EARG;
+  st = dispatch<true, EPI_ARGMAX>(p, units, mt, ntw, ksplit, stream);
   if (st) return st;
   argmax_finalize_kernel<<<M, 256, 0, stream>>>(pval, pidx, units, M, out_tok);
   QWEN_RETURN_LAUNCH();

@@ -84,9 +84,38 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const bf16_t* __restrict_
   out[i] = f2bf(mul_rn(s, u));
 }
 
+// psq[m, u] = sum of squares of x[m, 16u .. 16u+15] (fp32 over the bf16 values):
+// the per-16-column partials the normed projections read. One thread per 8
+// values; the two threads of a 16-column unit are adjacent lanes.
+__global__ void __launch_bounds__(256) sumsq16_kernel(const bf16_t* __restrict__ x, float* __restrict__ psq,
+                                                       long long chunks) {
+  const long long c = blockIdx.x * 256ll + threadIdx.x;
+  float s = 0.f;
+  if (c < chunks) {
+    float f[8];
+    unpack8(reinterpret_cast<const uint4*>(x)[c], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
+  }
+  s += __shfl_xor(s, 1, 64);
+  if (c < chunks && (c & 1) == 0) psq[c >> 1] = s;
+}
+
 }  // namespace
 
 extern "C" {
+
+// Partial sums of squares per 16 columns of a [M, K] bf16 matrix (K % 16 == 0).
+int qwen_sumsq16(const void* x, float* psq, int M, int K, hipStream_t stream) {
+  if (!x || !psq) return QWEN_ENULL;
+  if (M < 0 || K <= 0 || K % 16 != 0) return QWEN_EARG;
+  const long long chunks = (long long)M * (K / 8);
+  if (chunks == 0) return QWEN_OK;
+  const long long blocks = (chunks + 255) / 256;
+  if (blocks > 0x7fffffffLL) return QWEN_EARG;
+  sumsq16_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const bf16_t*)x, psq, chunks);
+  QWEN_RETURN_LAUNCH();
+}
 
 int qwen_rms_norm(const void* x, const void* w, void* y, int M, int N, float eps, hipStream_t stream) {
   if (!x || !w || !y) return QWEN_ENULL;

@@ -88,15 +88,18 @@ __global__ void __launch_bounds__(256) tile_weight_kernel(const bf16_t* __restri
 
 // out[m, :] = W[tok[m], :] read from the tiled (tied embedding / LM head) weight.
 // tok comes either from tok[m] or, for a decode step, from hist[m, pos[m]].
+// With psq != null it also writes the per-16-column sums of squares of each
+// row, which the first layer's normed QKV projection reads.
 // Ids outside [0, V) are clamped so the gather stays in bounds (the host
 // validates prompt ids before they reach the device).
 __global__ void __launch_bounds__(256) embed_kernel(const int64_t* __restrict__ tok, const int64_t* __restrict__ hist,
                                                     const int32_t* __restrict__ pos, int cap,
-                                                    const bf16_t* __restrict__ w, bf16_t* __restrict__ out, int M,
-                                                    long long V, int K) {
-  const long long c = blockIdx.x * 256ll + threadIdx.x;
+                                                    const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+                                                    float* __restrict__ psq, int M, long long V, int K) {
+  const long long c0 = blockIdx.x * 256ll + threadIdx.x;
   const int kc = K / 8;
-  if (c >= (long long)M * kc) return;
+  const bool live = c0 < (long long)M * kc;
+  const long long c = live ? c0 : 0;   // dead lanes redo chunk 0 so the pair shuffle stays uniform
   const int m = (int)(c / kc);
   const int chunk = (int)(c - (long long)m * kc);
   long long id;
@@ -112,7 +115,16 @@ __global__ void __launch_bounds__(256) embed_kernel(const int64_t* __restrict__ 
   const int r = (int)(id & 15);
   const int kt = chunk >> 2, q = chunk & 3;
   const long long src = ((nt * KT + kt) * 64 + q * 16 + r);
-  reinterpret_cast<uint4*>(out)[c] = reinterpret_cast<const uint4*>(w)[src];
+  const uint4 v = reinterpret_cast<const uint4*>(w)[src];
+  if (live) reinterpret_cast<uint4*>(out)[c] = v;
+  if (psq) {  // partial sums of squares per 16 columns (adjacent lane pairs), for the next RMSNorm
+    float f[8], s = 0.f;
+    unpack8(v, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
+    s += __shfl_xor(s, 1, 64);
+    if (live && (c & 1) == 0) psq[c >> 1] = s;
+  }
 }
 
 int grid_for(long long chunks, unsigned* blocks) {
@@ -160,13 +172,14 @@ int qwen_tile_weight(const void* src, void* dst, long long N, int K, int pair, h
 // Embedding gather from the tiled table. Either tok (M ids) or hist/pos
 // (token hist[m, pos[m]] of each of M rows, row stride cap) must be given.
 int qwen_embed(const int64_t* tok, const int64_t* hist, const int32_t* pos, int cap, const void* w_tiled, void* out,
-               int M, long long V, int K, hipStream_t stream) {
+               float* psq_out, int M, long long V, int K, hipStream_t stream) {
   if (!w_tiled || !out || (!tok && (!hist || !pos))) return QWEN_ENULL;
   if (M < 0 || V <= 0 || V % 16 != 0 || K <= 0 || K % 32 != 0 || (!tok && cap <= 0)) return QWEN_EARG;
   if (M == 0) return QWEN_OK;
   unsigned blocks;
   if (grid_for((long long)M * (K / 8), &blocks)) return QWEN_EARG;
-  embed_kernel<<<blocks, 256, 0, stream>>>(tok, hist, pos, cap, (const bf16_t*)w_tiled, (bf16_t*)out, M, V, K);
+  embed_kernel<<<blocks, 256, 0, stream>>>(tok, hist, pos, cap, (const bf16_t*)w_tiled, (bf16_t*)out, psq_out, M, V,
+                                           K);
   QWEN_RETURN_LAUNCH();
 }
 

@@ -267,11 +267,16 @@ class Engine:
                 "q": torch.empty((B, T, self.Nq, self.D), dtype=BF16, device=dev),
                 "a": torch.empty((B, T, self.Nq * self.D), dtype=BF16, device=dev),
                 "p": torch.empty((M, self.I), dtype=BF16, device=dev),
+                "psq": torch.empty((M, self.H // 16), dtype=torch.float32, device=dev),
                 "next": torch.empty((M,), dtype=torch.int64, device=dev),
                 "splits": S,
                 "attn_ws": torch.empty(max(4, ops.attn_workspace_bytes(B, T, self.Nq, self.Nkv, self.D, S)),
                                        dtype=torch.uint8, device=dev),
                 "lm_cfg": lm_cfg,
+                "cfg_qkv": ops.gemm_config(M, (self.Nq + 2 * self.Nkv) * self.D, self.H),
+                "cfg_o": ops.gemm_config(M, self.H, self.Nq * self.D),
+                "cfg_gu": ops.gemm_config(M, 2 * self.I, self.H, True),
+                "cfg_down": ops.gemm_config(M, self.H, self.I),
                 "lm_ws": torch.empty(ops.argmax_workspace_bytes(M, self.V, lm_cfg[0]), dtype=torch.uint8,
                                      device=dev),
             }
@@ -289,27 +294,28 @@ class Engine:
         B = self.B
         M = B * T
         b = self._buffers(B, T)
-        h, qkv, q, a, p = b["h"], b["qkv"], b["q"], b["a"], b["p"]
-        stream = torch.cuda.current_stream().cuda_stream
+        h, qkv, q, a, p, psq = b["h"], b["qkv"], b["q"], b["a"], b["p"], b["psq"]
+        # psq holds the per-16-column sums of squares of the current residual
+        # stream h: written by whoever last wrote h (embedding, O / down
+        # epilogues), read by the next normed projection.
         if tok is None:
             assert T == 1
-            ops._lib.call("qwen_embed", None, self.hist_buf.data_ptr(), self.pos_buf.data_ptr(), self.CAP,
-                          self.embed.data.data_ptr(), h.data_ptr(), M, self.V, self.H, stream)
+            ops.embed_hist(self.hist_buf, self.pos_buf, self.embed, h, psq_out=psq)
         else:
-            ops.embed(tok.reshape(-1), self.embed, out=h)
+            ops.embed(tok.reshape(-1), self.embed, out=h, psq_out=psq)
         for l, w in enumerate(self.layers):
-            ops.fused_linear(h, w.w_qkv, norm_w=w.ln1, eps=self.eps, out=qkv)
+            ops.fused_linear(h, w.w_qkv, b["cfg_qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq)
             ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
                                    self.k_cache[l], self.v_cache[l], out=q)
             ops.attn_decode(q, self.k_cache[l], self.v_cache[l], self.pos_buf, self.scale, b["splits"], len_add=T,
                             out=a, workspace=b["attn_ws"])
-            ops.fused_linear(a.view(M, -1), w.w_o, residual=h, out=h)
-            ops.fused_linear(h, w.w_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p)
-            ops.fused_linear(p, w.w_down, residual=h, out=h)
+            ops.fused_linear(a.view(M, -1), w.w_o, b["cfg_o"], residual=h, out=h, psq_out=psq)
+            ops.fused_linear(h, w.w_gu, b["cfg_gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, psq_in=psq)
+            ops.fused_linear(p, w.w_down, b["cfg_down"], residual=h, out=h, psq_out=psq)
             if hidden is not None:
                 hidden.append(h.clone())
         ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"], out=b["next"],
-                           workspace=b["lm_ws"])
+                           workspace=b["lm_ws"], psq_in=psq)
         return b["next"]
 
     def _plain_step(self):

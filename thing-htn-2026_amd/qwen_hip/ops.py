@@ -206,9 +206,26 @@ def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
     return t
 
 
+# Measured launch shapes (ntw, ksplit) for the Qwen3-4B projections on MI355X,
+# keyed by (N, K, SwiGLU pair) and by M <= 16 (one A fragment) or M <= 32 (two).
+_TUNED = {
+    (6144, 2560, False): {16: (1, 4), 32: (2, 4)},     # QKV
+    (2560, 4096, False): {16: (1, 16), 32: (1, 8)},    # O
+    (19456, 2560, True): {16: (2, 2), 32: (2, 2)},     # gate/up + SwiGLU
+    (2560, 9728, False): {16: (1, 16), 32: (1, 8)},    # down
+}
+
+
 def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, int]:
-    """(ntw, ksplit) launch shape: enough wavefronts to cover 256 CUs (about 2048),
-    at least 8 k-steps (8 KB of weight per n-tile) per wavefront."""
+    """(ntw, ksplit) launch shape for ``x[M, K] @ W[N, K]^T``.
+
+    Known Qwen3-4B shapes use the measured table; otherwise: enough wavefronts
+    to cover 256 CUs (about 2048), at least 8 k-steps (8 KB of weight per
+    n-tile) per wavefront.
+    """
+    tuned = _TUNED.get((N, K, bool(silu_pair)))
+    if tuned is not None:
+        return tuned[16 if M <= 16 else 32]
     ntw = 2 if silu_pair else 1
     units = N // (16 * ntw)
     KT = K // 32
@@ -220,16 +237,30 @@ def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, i
     return ntw, ks
 
 
+def sumsq16(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-16-column partial sums of squares ``[M, K/16]`` fp32 (the RMSNorm statistics)."""
+    _gpu(x)
+    assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous() and x.shape[1] % 16 == 0
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, K // 16), dtype=torch.float32, device=x.device)
+    _lib.call("qwen_sumsq16", x.data_ptr(), out.data_ptr(), M, K, _stream())
+    return out
+
+
 def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps: float = 0.0, residual=None,
-                 silu_pair: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+                 silu_pair: bool = False, out: torch.Tensor | None = None, psq_in: torch.Tensor | None = None,
+                 psq_out: torch.Tensor | None = None) -> torch.Tensor:
     """``x @ w.T`` with optional RMSNorm prologue and residual / SwiGLU epilogue (``gemm_fused.py:136-173``).
 
     ``x [M <= 32, K]`` bf16; ``w`` tiled ``[N, K]`` (for ``silu_pair`` a pair-
     interleaved ``cat(gate, up)`` and the output is ``[M, N/2]``); ``norm_w [K]``;
     ``residual [M, N]`` (may be the same tensor as ``out``). ``cfg`` is
-    ``(ntw, ksplit)`` or ``None`` for ``gemm_config``.
+    ``(ntw, ksplit)`` or ``None`` for ``gemm_config``. ``psq_in`` are x's
+    ``sumsq16`` partials (computed here when omitted); ``psq_out`` receives the
+    partials of a residual output.
     """
-    _gpu(x, norm_w, residual, out)
+    _gpu(x, norm_w, residual, out, psq_in, psq_out)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
     M, K = x.shape
     assert K == w.K and 1 <= M <= 32, f"x [{M}, {K}] vs weight K={w.K}; M must be in [1, 32]"
@@ -237,21 +268,27 @@ def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps:
     assert silu_pair == w.pair, "silu_pair requires a pair-interleaved weight (and only then)"
     if norm_w is not None:
         assert norm_w.dtype == BF16 and norm_w.numel() == K and norm_w.is_contiguous()
+        if psq_in is None:
+            psq_in = sumsq16(x)
+        assert psq_in.dtype == torch.float32 and psq_in.shape == (M, K // 16) and psq_in.is_contiguous()
     ncols = w.N // 2 if silu_pair else w.N
     if residual is not None:
         assert residual.shape == (M, ncols) and residual.dtype == BF16 and residual.is_contiguous()
+    if psq_out is not None:
+        assert residual is not None and psq_out.shape == (M, ncols // 16) and psq_out.dtype == torch.float32
     if out is None:
         out = torch.empty((M, ncols), dtype=BF16, device=x.device)
     assert out.shape == (M, ncols) and out.is_contiguous()
     ntw, ks = cfg if cfg is not None else gemm_config(M, w.N, K, silu_pair)
     epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
     _lib.call("qwen_linear", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols, _nullable(norm_w),
-              float(eps), _nullable(residual), epi, ntw, ks, _stream())
+              _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi, ntw, ks, _stream())
     return out
 
 
 def lm_head_config(M: int, N: int, K: int) -> tuple[int, int]:
-    return 2, 2
+    """(ntw, ksplit) for the LM head: the vocabulary gives thousands of workgroups already."""
+    return (2, 4) if M <= 16 else (2, 2)
 
 
 def argmax_workspace_bytes(M, N, ntw) -> int:
@@ -259,30 +296,44 @@ def argmax_workspace_bytes(M, N, ntw) -> int:
 
 
 def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWeight, *, cfg=None,
-                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                   psq_in: torch.Tensor | None = None) -> torch.Tensor:
     """Final RMSNorm + tied LM head + first-index argmax over bf16 logits -> int64 ``[M]``."""
-    _gpu(x, norm_w, out, workspace)
+    _gpu(x, norm_w, out, workspace, psq_in)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
     M, K = x.shape
     assert K == w.K and 1 <= M <= 32 and not w.pair
+    if psq_in is None:
+        psq_in = sumsq16(x)
     ntw, ks = cfg if cfg is not None else lm_head_config(M, w.N, K)
     need = argmax_workspace_bytes(M, w.N, ntw)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     if out is None:
         out = torch.empty((M,), dtype=torch.int64, device=x.device)
-    _lib.call("qwen_lm_head_argmax", x.data_ptr(), norm_w.data_ptr(), float(eps), w.data.data_ptr(), M, w.N, K,
-              workspace.data_ptr(), workspace.numel(), out.data_ptr(), ntw, ks, _stream())
+    _lib.call("qwen_lm_head_argmax", x.data_ptr(), norm_w.data_ptr(), psq_in.data_ptr(), float(eps),
+              w.data.data_ptr(), M, w.N, K, workspace.data_ptr(), workspace.numel(), out.data_ptr(), ntw, ks,
+              _stream())
     return out
 
 
-def embed(tok: torch.Tensor, w: TiledWeight, out: torch.Tensor | None = None) -> torch.Tensor:
+def embed(tok: torch.Tensor, w: TiledWeight, out: torch.Tensor | None = None,
+          psq_out: torch.Tensor | None = None) -> torch.Tensor:
     """``F.embedding(tok, W)`` from the tiled tied table; ``tok`` int64 ``[M]``."""
-    _gpu(tok)
+    _gpu(tok, psq_out)
     assert tok.dtype == torch.int64 and tok.is_contiguous()
     M = tok.numel()
     if out is None:
         out = torch.empty((M, w.K), dtype=BF16, device=tok.device)
-    _lib.call("qwen_embed", tok.data_ptr(), None, None, 0, w.data.data_ptr(), out.data_ptr(), M, w.N, w.K,
-              _stream())
+    _lib.call("qwen_embed", tok.data_ptr(), None, None, 0, w.data.data_ptr(), out.data_ptr(), _nullable(psq_out),
+              M, w.N, w.K, _stream())
+    return out
+
+
+def embed_hist(hist: torch.Tensor, pos: torch.Tensor, w: TiledWeight, out: torch.Tensor,
+               psq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-step embedding of ``hist[b, pos[b]]`` for every row ``b`` (``engine/engine.py:941-946``)."""
+    B, cap = hist.shape
+    _lib.call("qwen_embed", None, hist.data_ptr(), pos.data_ptr(), cap, w.data.data_ptr(), out.data_ptr(),
+              _nullable(psq_out), B, w.N, w.K, _stream())
     return out
