@@ -50,17 +50,31 @@ int qwen_qk_norm_rope_cache(const void* qkv, const void* q_norm_w, const void* k
                             const void* sin_tab, const int32_t* positions, void* q_out, void* k_cache, void* v_cache,
                             int B, int T, int Nq, int Nkv, int D, int CAP, int P, float eps, hipStream_t stream);
 
-/* Workspace bytes for qwen_attn_decode with the given split count. */
+/* Workspace bytes for qwen_attn_decode / qwen_attn_decode_fused with the given split count
+ * (0 for num_splits == 1). The workspace holds the split partials and one arrival counter per
+ * (sequence, KV head, query); it must be zero before its first use and every launch leaves the
+ * counters at zero again, so one buffer serves any number of launches on one stream. */
 long long qwen_attn_workspace_bytes(int B, int T, int Nq, int Nkv, int D, int num_splits);
 
 /* attn_decode(q [B, T, Nq, D], caches [B, Nkv, CAP, D], lengths [B] int32, scale, num_splits)
  * -> out [B, T, Nq*D]. The valid length of sequence b is lengths[b] + len_add (len_add = 0
- * gives the reference semantics; the engine passes positions with len_add = T).
- * Nq == 4 * Nkv, D == 128, 1 <= T <= 16.
+ * gives the reference semantics). Nq == 4 * Nkv, D == 128, 1 <= T <= 16; waves (1|2|4|8)
+ * wavefronts per workgroup split each context split further.
  * Replaces engine/kernels/attention.py:278-348 (attn_decode) / torch_ref.py:168-227. */
 int qwen_attn_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* lengths, int len_add,
                      void* out, void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
-                     int CAP, float scale, int num_splits, hipStream_t stream);
+                     int CAP, float scale, int num_splits, int waves, hipStream_t stream);
+
+/* The decode step's qk_norm_rope_cache + attn_decode in one launch: q heads are RMS-normed
+ * (q_norm_w) and rotated from qkv [B*T, (Nq+2Nkv)*D]; the T new keys at positions[b] + t are
+ * normed (k_norm_w), rotated and consumed from qkv and, with the raw V, written to the caches;
+ * lengths are positions[b] + T. cos/sin: [P, D] bf16 tables.
+ * Replaces engine/kernels/rope.py:169-226 followed by engine/kernels/attention.py:278-348
+ * (the two ops of engine/engine.py:1110-1113). */
+int qwen_attn_decode_fused(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                           const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                           void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
+                           int P, float eps, float scale, int num_splits, int waves, hipStream_t stream);
 
 /* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
  * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed
@@ -69,28 +83,36 @@ int qwen_attn_decode(const void* q, const void* k_cache, const void* v_cache, co
  * can emit it. */
 int qwen_sumsq16(const void* x, float* psq, int M, int K, hipStream_t stream);
 
+/* Workspace bytes for qwen_linear with ks > 1 (0 for ks == 1): split-K partials plus one
+ * arrival counter per n-tile group; zero before first use, left at zero by every launch. */
+long long qwen_linear_workspace_bytes(int M, int N, int ntw, int ks);
+
 /* out = x @ W^T with optional RMSNorm prologue (norm_w != NULL; psq_in = x's
  * qwen_sumsq16 partials [M, K/16]) and epilogue
  * epi = 0 store, 1 residual add (out = bf16(residual + bf16(acc)); residual may alias out;
  * psq_out != NULL also writes the new rows' [M, N/16] partials),
  * 2 SwiGLU pair (W tiled with pair interleave; N = 2I rows; out has I columns).
- * x: [M, K] (M <= 32), W tiled [N, K]. ntw (1|2) n-tiles and ksplit (1|2|4|8|16)
- * wavefronts per workgroup select the launch shape.
- * Replaces the projections of engine/engine.py:1108-1118 (_mm / F.linear) and
+ * x: [M, K] (M <= 32), W tiled [N, K]. Launch shape: ntw (1|2|4) n-tiles per workgroup,
+ * waves (4|8|16) wavefronts per workgroup, ks k-splits across workgroups (ks > 1 needs the
+ * workspace). Replaces the projections of engine/engine.py:1108-1118 (_mm / F.linear) and
  * engine/kernels/gemm_fused.py:136-173 (fused_linear). */
 int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* norm_w,
-                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int ksplit,
-                hipStream_t stream);
-
-/* Workspace bytes for qwen_lm_head_argmax. */
-long long qwen_argmax_workspace_bytes(int M, int N, int ntw);
+                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int waves,
+                int ks, void* workspace, long long workspace_bytes, hipStream_t stream);
 
 /* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
- * out_tok[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.
+ * token[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.
+ * The result is folded into amax[m] (uint64: monotone logit bits << 32 | ~index), which must
+ * be zero before the call; with out_tok != NULL the tokens are extracted into out_tok [M]
+ * int64 and amax re-armed, otherwise qwen_decode_finish / qwen_argmax_extract consume it.
  * Replaces engine/engine.py:1119-1121 (final add_rms_norm, lm_head _mm, argmax). */
 int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, float eps, const void* w_tiled, int M,
-                        int N, int K, void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw,
-                        int ksplit, hipStream_t stream);
+                        int N, int K, unsigned long long* amax, int64_t* out_tok, int ntw, int waves,
+                        hipStream_t stream);
+
+/* out[m] = token index held in amax[m] (from qwen_lm_head_argmax); re-arms amax to zero.
+ * Replaces the argmax(-1) read-out of engine/engine.py:1121. */
+int qwen_argmax_extract(unsigned long long* amax, int M, int64_t* out, hipStream_t stream);
 
 /* Embedding gather from the tiled tied table: out[m] = W[tok[m]], or, with tok == NULL,
  * out[m] = W[hist[m, pos[m]]] (the decode step's token read, engine/engine.py:941-946).
@@ -99,11 +121,14 @@ int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, 
 int qwen_embed(const int64_t* tok, const int64_t* hist, const int32_t* pos, int cap, const void* w_tiled, void* out,
                float* psq_out, int M, long long V, int K, hipStream_t stream);
 
-/* Token bookkeeping after a plain decode step: hist[b, pos[b]+1] = next[b], pos[b] += 1,
- * frozen rows ((pos+1 - s_buf) >= ntarget) write slot cap-1 and keep pos.
- * Replaces the tail of engine/engine.py:941-953 (_plain_step). */
-int qwen_plain_update(const int64_t* next, int64_t* hist, int32_t* pos, const int64_t* s_buf, const int64_t* ntarget,
-                      int B, int cap, hipStream_t stream);
+/* Step tail after the LM head: token[b] = index held in amax[b] (re-armed to zero) -> next[b];
+ * hist[b, pos[b]+1] = token[b], pos[b] += 1, frozen rows ((pos+1 - s_buf) >= ntarget) write slot
+ * cap-1 and keep pos; then h[b] = W[hist[b, pos[b]]] from the tiled table and psq its
+ * qwen_sumsq16 partials (the next step's input). Replaces the tail of engine/engine.py:941-953
+ * (_plain_step) and the embedding of engine/engine.py:1101. */
+int qwen_decode_finish(unsigned long long* amax, int64_t* next, int64_t* hist, int32_t* pos, const int64_t* s_buf,
+                       const int64_t* ntarget, const void* w_tiled, void* h, float* psq, int B, int cap, long long V,
+                       int K, hipStream_t stream);
 
 /* Row-major [N, K] bf16 -> tiled layout (pair = 1: gate|up interleave, tile 2p = rows
  * 16p.., tile 2p+1 = rows N/2 + 16p..). Replaces the weight fusion / layout step of

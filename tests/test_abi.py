@@ -49,9 +49,16 @@ def test_workspace_queries_run_without_gpu():
     from qwen_hip import _lib
     if not os.path.exists(_lib.LIB_PATH):
         pytest.skip("libqwen_hip.so not built")
-    assert _lib.query("qwen_attn_workspace_bytes", 1, 1, 32, 8, 128, 4) == 1 * 8 * 4 * 4 * (2 + 128) * 4
-    assert _lib.query("qwen_argmax_workspace_bytes", 1, 151936, 2) == (151936 // 32) * 8
+    # one counter per row (padded to 256 B), then split partials (m, l, acc[128]) per (row, split, head)
+    assert _lib.query("qwen_attn_workspace_bytes", 1, 1, 32, 8, 128, 4) == 1 * 8 * 4 * 4 * (2 + 128) * 4 + 256
+    assert _lib.query("qwen_attn_workspace_bytes", 1, 1, 32, 8, 128, 1) == 0      # one split: no workspace
     assert _lib.query("qwen_attn_workspace_bytes", 0, 1, 32, 8, 128, 4) == 0
+    # split-K: a fixed counter region, then units * ks * (MT * ntw) fragments of 1 KB
+    units = 2560 // 16
+    counters = 65536     # fixed region: GEMMs of any shape share one workspace
+    assert _lib.query("qwen_linear_workspace_bytes", 1, 2560, 1, 4) == units * 4 * 1024 + counters
+    assert _lib.query("qwen_linear_workspace_bytes", 32, 2560, 1, 4) == units * 4 * 2048 + counters
+    assert _lib.query("qwen_linear_workspace_bytes", 8, 2560, 1, 1) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -162,6 +162,59 @@ def test_attn_kv_head_mapping(qops):
         assert torch.equal(got[0, 0, h], torch.full((D,), float(h // 4 + 1), dtype=BF16))
 
 
+@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("splits", [1, 3, 16])
+def test_attn_decode_waves_and_splits(qops, waves, splits):
+    g = torch.Generator().manual_seed(123)
+    B, T, NQ, NKV, D, CAP = 3, 2, 32, 8, 128, 640
+    lengths = [600, 37, 2]
+    q = _bf16(B, T, NQ, D, gen=g)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    lens = torch.tensor(lengths, dtype=torch.int32)
+    want = R.attn_decode(q, kc, vc, lens, D ** -0.5)
+    ws = qops.attn_workspace(B, T, NQ, NKV, D, splits, DEV)
+    for _ in range(2):   # second launch on the same workspace: split counters re-armed
+        got = qops.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), lens.to(DEV), D ** -0.5, splits, workspace=ws,
+                               waves=waves).cpu()
+        assert_close(got, want, 2e-2, 0, f"waves={waves} splits={splits}")
+
+
+@pytest.mark.parametrize("B,T,positions,splits,waves", [
+    (1, 1, [0], 1, 8), (1, 1, [383], 1, 8), (1, 1, [383], 4, 8), (2, 1, [5, 900], 8, 2), (4, 5, [4096, 100, 7, 0], 4, 8),
+    (3, 16, [16, 200, 1000], 2, 4), (8, 1, [2304, 1, 77, 2048, 999, 1500, 64, 65], 16, 8)])
+def test_attn_decode_fused_matches_rope_then_attention(qops, B, T, positions, splits, waves):
+    """One launch == the reference's qk_norm_rope_cache followed by attn_decode (oracle), including
+    the cache writes; every other cache slot is left untouched."""
+    g = torch.Generator().manual_seed(77 + B * T)
+    NQ, NKV, D, CAP = 32, 8, 128, 4160
+    cos, sin = R.rope_tables(8192, 5e6, D)
+    qkv = _bf16(B * T, (NQ + 2 * NKV) * D, gen=g, scale=2.0)
+    kc, vc = _bf16(B, NKV, CAP, D, gen=g), _bf16(B, NKV, CAP, D, gen=g)
+    qw, kw = _gain(D, g), _gain(D, g)
+    pos = torch.tensor(positions, dtype=torch.int32)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    q_ref = R.qk_norm_rope_cache(qkv, qw, kw, EPS, cos, sin, pos, T, kc_ref, vc_ref)
+    want = R.attn_decode(q_ref, kc_ref, vc_ref, pos + T, D ** -0.5)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    got = qops.attn_decode_fused(qkv.to(DEV), qw.to(DEV), kw.to(DEV), EPS, cos.to(DEV), sin.to(DEV), pos.to(DEV), T,
+                                 kd, vd, D ** -0.5, splits, waves=waves).cpu()
+    assert got.shape == (B, T, NQ * D)
+    # q and k pass through RoPE, whose bf16(p1 + p2) can cancel: a one-ulp change of the
+    # normed input (fp32 order of the sum of squares) moves a few q/k elements by several
+    # ulps, and the output inherits it. Bar: the reference's attention-variant tolerance
+    # (tests/test_torch_ref.py:421, atol = rtol = 2e-2), with at most 0.1% of the outputs
+    # outside the tighter unfused bar (atol 2e-2).
+    assert_close(got, want, 2e-2, 2e-2, "fused attention")
+    assert float(((got.float() - want.float()).abs() > 2e-2).float().mean()) <= 1e-3
+    assert_close(kd.cpu(), kc_ref, 1e-2, 1 / 64, "k_cache")
+    assert float((kd.cpu() != kc_ref).float().mean()) <= 1e-2
+    assert torch.equal(vd.cpu(), vc_ref)     # V copied raw; every other slot untouched
+    untouched = torch.ones(B, CAP, dtype=torch.bool)
+    for b, p0 in enumerate(positions):
+        untouched[b, p0:p0 + T] = False
+    assert torch.equal(kd.cpu().permute(0, 2, 1, 3)[untouched], kc.permute(0, 2, 1, 3)[untouched])
+
+
 # ---------------------------------------------------------------- weights
 
 @pytest.mark.parametrize("N,K,pair", [(64, 64, False), (6144, 2560, False), (256, 96, True)])
@@ -224,14 +277,85 @@ def test_fused_linear(qops, M, kind):
     assert_close(got, want, 1e-2, 1 / 64, kind)
 
 
-@pytest.mark.parametrize("ntw,ks", [(1, 1), (1, 2), (1, 4), (1, 8), (1, 16), (2, 1), (2, 4), (2, 8)])
-def test_fused_linear_launch_shapes_agree(qops, ntw, ks):
+@pytest.mark.parametrize("M", [5, 20])
+@pytest.mark.parametrize("ntw,waves,ks", [(1, 4, 1), (1, 8, 1), (1, 16, 1), (1, 8, 4), (1, 16, 8), (2, 8, 2),
+                                          (2, 4, 16), (4, 4, 4), (4, 8, 1), (1, 4, 64)])
+def test_fused_linear_launch_shapes_agree(qops, M, ntw, waves, ks):
     g = torch.Generator().manual_seed(9)
-    M, N, K = 5, 256, 9728
+    N, K = 256, 9728
     x, w = _bf16(M, K, gen=g), _bf16(N, K, gen=g, scale=0.05)
     t = qops.tile_weight(w.to(DEV))
-    got = qops.fused_linear(x.to(DEV), t, cfg=(ntw, ks)).cpu()
-    assert_close(got, R.linear(x, w), 1e-2, 1 / 64, f"ntw={ntw} ks={ks}")
+    if M > 16 and (ntw, waves) == (1, 16):
+        # not built (two A fragments x 16 wavefronts would spill): a clear error, no launch
+        with pytest.raises(RuntimeError, match="bad size/shape"):
+            qops.fused_linear(x.to(DEV), t, cfg=(ntw, waves, ks))
+        return
+    got = qops.fused_linear(x.to(DEV), t, cfg=(ntw, waves, ks)).cpu()
+    assert_close(got, R.linear(x, w), 1e-2, 1 / 64, f"ntw={ntw} waves={waves} ks={ks}")
+
+
+@pytest.mark.parametrize("kind,cfg", [("res", (1, 8, 8)), ("silu", (2, 8, 4)), ("silu", (4, 4, 2)),
+                                      ("norm", (1, 4, 5))])
+def test_fused_linear_split_k_epilogues(qops, kind, cfg):
+    """Split-K across workgroups (last-arriver reduction) with each fused epilogue, run twice on
+    one workspace: the arrival counters must be re-armed, and the results identical."""
+    g = torch.Generator().manual_seed(55)
+    M = 7
+    N, K = (512, 2560) if kind != "res" else (256, 4096)
+    x = _bf16(M, K, gen=g)
+    w = _bf16(N, K, gen=g, scale=0.05)
+    nw = _gain(K, g) if kind in ("norm", "silu") else None
+    resid = _bf16(M, N, gen=g) if kind == "res" else None
+    xin = R.rms_norm(x, nw, EPS) if nw is not None else x
+    y = R.linear(xin, w)
+    want = R.silu_mul(y) if kind == "silu" else y
+    if resid is not None:
+        want = (resid.float() + want.float()).to(BF16)
+    t = qops.tile_weight(w.to(DEV), pair=kind == "silu")
+    ws = qops.linear_workspace(qops.linear_workspace_bytes(M, N, cfg[0], cfg[2]), DEV)
+    outs = []
+    for _ in range(2):
+        r = None if resid is None else resid.to(DEV)
+        psq = torch.empty((M, N // 16), dtype=torch.float32, device=DEV) if kind == "res" else None
+        out = qops.fused_linear(x.to(DEV), t, cfg, norm_w=None if nw is None else nw.to(DEV), eps=EPS, residual=r,
+                                out=r, psq_out=psq, silu_pair=kind == "silu", workspace=ws)
+        outs.append(out.cpu())
+        if psq is not None:   # the epilogue's statistics are those of the rounded output rows
+            assert_close(psq.cpu(), qops.sumsq16(out).cpu(), 1e-5, 1e-6, "psq_out")
+    assert_close(outs[0], want, 1e-2, 1 / 64, kind)
+    assert torch.equal(outs[0], outs[1])
+    assert int(ws[:65536].count_nonzero()) == 0, "split-K arrival counters not re-armed"
+
+
+@pytest.mark.parametrize("M", [1, 7, 20, 32])
+@pytest.mark.parametrize("kind,N,K,ntw", [("norm", 6144, 2560, 1), ("norm", 6144, 2560, 2), ("res", 2560, 4096, 1),
+                                          ("silu", 19456, 2560, 2), ("res", 2560, 9728, 1)])
+def test_fused_linear_stream_k(qops, M, kind, N, K, ntw):
+    """Stream-K launch (one workgroup per CU, units shared between CUs finished by the last
+    arriver) on the Qwen3-4B projection shapes, twice on one workspace."""
+    g = torch.Generator().manual_seed(1000 + M + N)
+    x = _bf16(M, K, gen=g)
+    w = _bf16(N, K, gen=g, scale=0.03)
+    nw = _gain(K, g) if kind in ("norm", "silu") else None
+    ncol = N // 2 if kind == "silu" else N
+    resid = _bf16(M, ncol, gen=g) if kind == "res" else None
+    xin = R.rms_norm(x, nw, EPS) if nw is not None else x
+    y = R.linear(xin, w)
+    want = R.silu_mul(y) if kind == "silu" else y
+    if resid is not None:
+        want = (resid.float() + want.float()).to(BF16)
+    t = qops.tile_weight(w.to(DEV), pair=kind == "silu")
+    cfg = (ntw, 8, 0)
+    ws = qops.linear_workspace(qops.linear_workspace_bytes(M, N, ntw, 0), DEV)
+    outs = []
+    for _ in range(2):
+        r = None if resid is None else resid.to(DEV)
+        out = qops.fused_linear(x.to(DEV), t, cfg, norm_w=None if nw is None else nw.to(DEV), eps=EPS, residual=r,
+                                out=r, silu_pair=kind == "silu", workspace=ws)
+        outs.append(out.cpu())
+    assert_close(outs[0], want, 1e-2, 1 / 64, f"{kind} {N}x{K} M={M}")
+    assert torch.equal(outs[0], outs[1])
+    assert int(ws[:65536].count_nonzero()) == 0, "arrival counters not re-armed"
 
 
 def test_fused_linear_two_hot_exact(qops):
@@ -284,3 +408,58 @@ def test_lm_head_argmax_random(qops, M):
     assert bool(((top - chosen) <= ulp).all())
     exact = (top - logits.topk(2, -1).values[:, 1]) > 2 * ulp
     assert torch.equal(got[exact], logits.argmax(-1)[exact])
+
+
+# ---------------------------------------------------------------- step tail
+
+def _argmax_key(value: float, index: int) -> int:
+    """Host restatement of the packed key: monotone fp32 bits << 32 | (2^32 - 1 - index)."""
+    u = int(np.array([value], dtype=np.float32).view(np.uint32)[0])
+    hi = (~u & 0xFFFFFFFF) if u & 0x80000000 else (u | 0x80000000)
+    key = (hi << 32) | (0xFFFFFFFF - index)
+    return key - (1 << 64) if key >= (1 << 63) else key      # as int64
+
+
+def test_decode_finish_updates_history_and_embeds(qops):
+    g = torch.Generator().manual_seed(4)
+    V, K, B, cap = 96, 64, 3, 16
+    table = _bf16(V, K, gen=g)
+    t = qops.tile_weight(table.to(DEV))
+    toks = [17, 95, 0]
+    keys = torch.tensor([_argmax_key(1.5, toks[0]), _argmax_key(-0.25, toks[1]), _argmax_key(0.0, toks[2])],
+                        dtype=torch.int64, device=DEV)
+    hist = torch.randint(0, V, (B, cap), generator=g)
+    pos = torch.tensor([3, 9, 12], dtype=torch.int32)
+    s_buf = torch.tensor([3], dtype=torch.int64)
+    ntarget = torch.tensor([9], dtype=torch.int64)      # row 2: (12 + 1 - 3) >= 9 -> frozen
+    hd, pd = hist.to(DEV), pos.to(DEV)
+    nxt = torch.empty(B, dtype=torch.int64, device=DEV)
+    h = torch.empty(B, K, dtype=BF16, device=DEV)
+    psq = torch.empty(B, K // 16, dtype=torch.float32, device=DEV)
+    qops.decode_finish(keys, nxt, hd, pd, s_buf.to(DEV), ntarget.to(DEV), t, h, psq)
+    assert nxt.cpu().tolist() == toks
+    assert int(keys.count_nonzero()) == 0               # re-armed for the next LM head
+    want_hist, want_pos = hist.clone(), pos.clone()
+    want_hist[0, 4], want_hist[1, 10], want_hist[2, cap - 1] = toks[0], toks[1], toks[2]
+    want_pos[0], want_pos[1] = 4, 10
+    assert torch.equal(hd.cpu(), want_hist) and torch.equal(pd.cpu(), want_pos)
+    rows = [toks[0], toks[1], int(want_hist[2, 12])]    # frozen row re-embeds hist[pos]
+    assert torch.equal(h.cpu(), table[rows])
+    assert_close(psq.cpu(), table[rows].float().pow(2).view(B, K // 16, 16).sum(-1), 1e-5, 1e-6, "psq")
+
+
+def test_lm_head_keys_then_extract(qops):
+    """extract=False leaves packed keys that argmax_extract decodes (and re-arms)."""
+    M, V, K = 3, 4096, 256
+    g = torch.Generator().manual_seed(8)
+    x = _bf16(M, K, gen=g)
+    nw = _gain(K, g)
+    w = _bf16(V, K, gen=g, scale=0.05)
+    t = qops.tile_weight(w.to(DEV))
+    want = qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, t).cpu()
+    keys = qops.argmax_keys(M, DEV)
+    qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, t, keys=keys, extract=False)
+    out = torch.empty(M, dtype=torch.int64, device=DEV)
+    qops.argmax_extract(keys, M, out)
+    assert torch.equal(out.cpu(), want)
+    assert int(keys.count_nonzero()) == 0

@@ -9,99 +9,148 @@
 //   EPI_STORE : out = bf16(acc)
 //   EPI_RES   : out = bf16(res + bf16(acc))      (residual add, in place allowed)
 //   EPI_SWIGLU: out = bf16(bf16(silu(bf16(g))) * bf16(u)) for a gate/up tile pair
-//   EPI_ARGMAX: logits = bf16(acc); per-row (max, lowest index) partials per
-//               workgroup, reduced by argmax_finalize_kernel (LM head + argmax,
-//               engine/engine.py:1119-1121).
+//   EPI_ARGMAX: logits = bf16(acc); the row's (max logit, lowest index) is folded
+//               into a packed 64-bit key with one atomicMax per row and workgroup
+//               (LM head + argmax, engine/engine.py:1119-1121).
 //
 // Weight layout ("MFMA-B tiles", written by weights.hip): W is cut into tiles
 // of 16 rows x 32 k; tile (nt, kt) is 1 KB at offset (nt * K/32 + kt) * 512
 // elements and lane l = 16*q + r of a wavefront owns the 16 bytes
 // W[16*nt + r][32*kt + 8*q .. +8] at tile offset 8*l. One global_load_dwordx4
 // per lane therefore reads a whole tile (1 KB contiguous) straight into the
-// B-operand registers of v_mfma_f32_16x16x32_bf16, and the k-reduction
-// happens inside the matrix core: no cross-lane shuffles, and the activation
-// traffic does not grow with M. M <= 16 rows use one A fragment (rows past M
-// are zero lanes), 17..32 rows use two.
+// B-operand registers of v_mfma_f32_16x16x32_bf16; the k-reduction happens in
+// the matrix core. Weights are read with non-temporal loads: every byte is used
+// once per step, and keeping it out of the memory-side cache raises the
+// sustained HBM read rate on MI355X (measured 7.0 vs 6.2 TB/s for a plain
+// streaming read). M <= 16 rows use one A fragment, 17..32 rows use two.
 //
-// Work decomposition: one workgroup per "unit" of NTW adjacent n-tiles;
-// its KSPLIT wavefronts split K into contiguous ranges and are reduced through
-// LDS in a fixed order (deterministic), then wavefront 0 runs the epilogue.
+// Work decomposition: the N/16 n-tiles are grouped NTW per "unit"; each unit's
+// K range is split over KS workgroups, and each workgroup's range over its WPG
+// wavefronts. Wavefront partials are reduced through LDS in a fixed order.
+// With KS > 1 every workgroup stores its fp32 partial with device-coherent
+// (sc1) stores, then bumps the unit's arrival counter; the last arriver reads
+// the KS partials back with sc1 loads, sums them in split order (so the result
+// does not depend on arrival order), runs the epilogue and re-arms the counter
+// to zero. No full-cache fences are needed because every value that crosses
+// workgroups travels with device-scope stores and loads.
 #include "common.h"
 
 namespace {
 
 enum { EPI_STORE = 0, EPI_RES = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
+// Split-K workspace: arrival counters for up to 16384 n-tile groups, then partials.
+constexpr long long QWEN_LINEAR_COUNTER_BYTES = 65536;
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 struct GemmParams {
-  const bf16_t* x;    // [M, K] row-major
-  const bf16_t* w;    // MFMA-B tiled weight, N x K
-  const bf16_t* nw;   // [K] RMSNorm gain (NORM)
-  const bf16_t* res;  // [M, ld_out] residual (EPI_RES)
-  bf16_t* out;        // [M, ld_out]
-  float* pval;        // [units, M] argmax partial values (EPI_ARGMAX)
-  int32_t* pidx;      // [units, M] argmax partial indices
+  const bf16_t* x;      // [M, K] row-major
+  const bf16_t* w;      // MFMA-B tiled weight, N x K
+  const bf16_t* nw;     // [K] RMSNorm gain (NORM)
+  const bf16_t* res;    // [M, ld_out] residual (EPI_RES)
+  bf16_t* out;          // [M, ld_out]
+  unsigned long long* amax;  // [M] packed (logit, index) keys (EPI_ARGMAX), zero before the launch
   const float* psq_in;  // [M, K/16] partial sums of squares of x per 16 columns (NORM)
   float* psq_out;       // [M, N/16] same for the output rows (EPI_RES, may be null)
-  int M, N, K, ld_out;
+  f32x4_t* part;        // [units * KS][MT*NTW][64] split-K partials (KS > 1)
+  unsigned* cnt;        // [units] arrival counters, zero between launches (KS > 1)
+  int M, N, K, ld_out, ks;
+  int piece_stride;     // partial slots per unit in `part` (ks for split-K, SK_PIECES for stream-K)
   float eps;
 };
 
-template <int MT, int NTW, int KSPLIT, bool NORM, int EPI>
-__global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) {
-  constexpr int U = 8;  // k-steps (1 KB tiles per n-tile) loaded ahead per wavefront
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int r = lane & 15, q = lane >> 4;
-  const int unit = blockIdx.x;
-  const int KT = p.K >> 5;
-  const int kpw = (KT + KSPLIT - 1) / KSPLIT;
-  const int k0 = min(KT, wave * kpw);
-  const int k1 = min(KT, k0 + kpw);
+__device__ __forceinline__ uint4 load_nt(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
-  __shared__ f32x4_t red[KSPLIT > 1 ? KSPLIT * MT * NTW * 64 : 1];
+// Device-coherent store / load of one fp32x4 (each component is a relaxed
+// agent-scope atomic access: global_store/load with sc1, no cache flush).
+__device__ __forceinline__ void store_dev(f32x4_t* p, const f32x4_t& v) {
+  float* f = reinterpret_cast<float*>(p);
+  __hip_atomic_store(f + 0, v[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(f + 1, v[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(f + 2, v[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(f + 3, v[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-  // Rows of the A operand this lane feeds: m = r + 16*mt. Rows past M read
-  // row 0 (always valid) and are zeroed, so the loads need no branch.
+__device__ __forceinline__ f32x4_t load_dev(const f32x4_t* p) {
+  const float* f = reinterpret_cast<const float*>(p);
+  return f32x4_t{__hip_atomic_load(f + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(f + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(f + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(f + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+}
+
+// Monotone map of an fp32 value onto uint32 (larger float -> larger integer).
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The A operand of one wavefront: rows m = r + 16*mt of x (rows past M read
+// row 0, the same cache lines as a live row, and are zeroed, so the loads need
+// no branch), and with NORM the RMSNorm factor of each row.
+template <int MT, bool NORM>
+struct AOperand {
   const bf16_t* xrow[MT];
   bool mval[MT];
+  float rinv[MT];
+
+  __device__ __forceinline__ void init(const GemmParams& p, int r, int q) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = r + 16 * mt;
-    mval[mt] = m < p.M;
-    xrow[mt] = p.x + (size_t)(mval[mt] ? m : 0) * p.K + 8 * q;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = r + 16 * mt;
+      mval[mt] = m < p.M;
+      xrow[mt] = p.x + (size_t)(mval[mt] ? m : 0) * p.K + 8 * q;
+    }
   }
 
   // RMSNorm statistics: the producer of x left one partial sum of squares per
   // 16 columns (rounded bf16 values, squared and summed in fp32). The four
-  // lanes of a row each add a quarter of them in a fixed order, so every
-  // workgroup derives bit-identical factors.
-  float rinv[MT];
-  if constexpr (NORM) {
-    const int nu = p.K >> 4;
+  // lanes of a row each add a contiguous quarter of them in a fixed order,
+  // then the quarters are combined by a fixed butterfly, so every workgroup
+  // derives bit-identical factors. The quarter is read with float4 loads that
+  // are all issued before the first add (out-of-range slots add zero).
+  __device__ __forceinline__ void stats(const GemmParams& p, int r, int q) {
+    if constexpr (NORM) {
+      const int nu = p.K >> 4;
+      const int per = nu >> 2;
+      constexpr int MAXV = 10;  // float4 loads per lane: up to 40 partials (K <= 2560)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float* ps = p.psq_in + (size_t)(mval[mt] ? r + 16 * mt : 0) * nu;
-      float s = 0.f;
-      for (int u = q; u < nu; u += 4) s += ps[u];
-      s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
+      for (int mt = 0; mt < MT; ++mt) {
+        const float* ps = p.psq_in + (size_t)(mval[mt] ? r + 16 * mt : 0) * nu;
+        float s = 0.f;
+        if ((nu & 15) == 0 && per <= 4 * MAXV) {
+          const float4* p4 = reinterpret_cast<const float4*>(ps + q * per);
+          const int n4 = per >> 2;
+          float4 v[MAXV];
+#pragma unroll
+          for (int j = 0; j < MAXV; ++j) v[j] = p4[min(j, n4 - 1)];
+#pragma unroll
+          for (int j = 0; j < MAXV; ++j) {
+            const float keep = j < n4 ? 1.f : 0.f;
+            s += v[j].x * keep;
+            s += v[j].y * keep;
+            s += v[j].z * keep;
+            s += v[j].w * keep;
+          }
+        } else {
+          for (int u = q * per; u < (q + 1) * per; ++u) s += ps[u];
+          if (nu & 3) {  // the last nu % 4 partials belong to lane q = 3
+            for (int u = 4 * per; u < nu; ++u) s += q == 3 ? ps[u] : 0.f;
+          }
+        }
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
+      }
     }
   }
 
-  f32x4_t acc[MT][NTW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const uint4* wt = reinterpret_cast<const uint4*>(p.w);
-  size_t wrow[NTW];
-#pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) wrow[nt] = (size_t)(unit * NTW + nt) * KT * 64 + lane;
-  const uint4* nwp = reinterpret_cast<const uint4*>(p.nw);
-
-  auto make_a = [&](uint4 raw, const uint4& gain, int mt) -> bf16x8_t {
+  // bf16x8 A fragment: raw x, or with NORM bf16(bf16(x * rinv) * gain).
+  __device__ __forceinline__ bf16x8_t make(uint4 raw, const uint4& gain, int mt) const {
     if (!mval[mt]) raw = make_uint4(0, 0, 0, 0);
     if constexpr (NORM) {
       float f[8], g[8], o[8];
@@ -113,71 +162,86 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
     } else {
       return as_bf16x8(raw);
     }
-  };
+  }
+};
 
-  // Each batch issues all of its loads first (weights from HBM, activations and
-  // gains from L2), then runs the MFMAs in arrival order. The last batch of a
-  // range is padded by re-reading step k1-1 (a cache hit) with a zero A
-  // operand, so there is no serial remainder loop.
-  for (int kt = k0; kt < k1; kt += U) {
+// Software-pipelined accumulation of k-steps [k0, k1) of one n-tile group:
+// a batch is U k-steps of loads (weights from HBM with non-temporal loads,
+// activations and gains from L2); the next batch is issued before the current
+// one is consumed, so two batches are in flight per wavefront. Steps past k1
+// re-read step k1-1 (a cache hit) and meet a zero A operand, so there is no
+// serial remainder loop. With `stats_after_first` the A operand's RMSNorm
+// statistics are computed once the first weights are in flight.
+template <int MT, int NTW, int U, bool NORM>
+__device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NORM>& A, size_t unit, int k0, int k1,
+                                           f32x4_t (&acc)[MT][NTW], int r, int q, int lane, bool stats_after_first) {
+  const uint4* wt = reinterpret_cast<const uint4*>(p.w);
+  const uint4* nwp = reinterpret_cast<const uint4*>(p.nw);
+  const size_t KT = p.K >> 5;
+  size_t wrow[NTW];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) wrow[nt] = (unit * NTW + nt) * KT * 64 + lane;
+  struct Batch {
     uint4 bt[U][NTW], at[U][MT], gt[U];
+  };
+  auto issue = [&](Batch& b, int kt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = min(kt + u, k1 - 1);
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) bt[u][nt] = wt[wrow[nt] + (size_t)kk * 64];
+      for (int nt = 0; nt < NTW; ++nt) b.bt[u][nt] = load_nt(wt + wrow[nt] + (size_t)kk * 64);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = min(kt + u, k1 - 1);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) at[u][mt] = *reinterpret_cast<const uint4*>(xrow[mt] + kk * 32);
-      if constexpr (NORM) gt[u] = nwp[kk * 4 + q];
+      for (int mt = 0; mt < MT; ++mt) b.at[u][mt] = *reinterpret_cast<const uint4*>(A.xrow[mt] + kk * 32);
+      if constexpr (NORM) b.gt[u] = nwp[kk * 4 + q];
     }
+  };
+  auto consume = [&](const Batch& b, int kt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool live = kt + u < k1;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        bf16x8_t a = make_a(at[u][mt], gt[u], mt);
+        bf16x8_t a = A.make(b.at[u][mt], b.gt[u], mt);
         if (!live) a = as_bf16x8(make_uint4(0, 0, 0, 0));
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bt[u][nt]), acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b.bt[u][nt]), acc[mt][nt], 0, 0, 0);
       }
     }
+  };
+  Batch b0, b1;
+  if (k0 < k1) issue(b0, k0);
+  if (stats_after_first) A.stats(p, r, q);
+  for (int kt = k0; kt < k1; kt += 2 * U) {
+    if (kt + U < k1) issue(b1, kt + U);
+    consume(b0, kt);
+    if (kt + U >= k1) break;
+    if (kt + 2 * U < k1) issue(b0, kt + 2 * U);
+    consume(b1, kt + U);
   }
+}
 
-  if constexpr (KSPLIT > 1) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) red[((wave * MT + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) {
-        f32x4_t s = red[(mt * NTW + nt) * 64 + lane];
-        for (int w = 1; w < KSPLIT; ++w) s += red[((w * MT + mt) * NTW + nt) * 64 + lane];
-        acc[mt][nt] = s;
-      }
-  }
-
-  // Epilogue. Lane (q, r) holds D[16*mt + 4*q + i][16*(unit*NTW + nt) + r].
+// Epilogue of one n-tile group (unit). Lane (q, r) holds D[16*mt + 4*q + i][16*(unit*NTW + nt) + r].
+template <int MT, int NTW, int EPI>
+__device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int lane) {
+  const int r = lane & 15, q = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * mt + 4 * q + i;
+      const bool mok = m < p.M;
       if constexpr (EPI == EPI_ARGMAX) {
         float best = -INFINITY;
         int bidx = 0x7fffffff;
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
           const float v = rbf(acc[mt][nt][i]);
-          const int col = (unit * NTW + nt) * 16 + r;
+          const int col = (int)(unit * NTW + nt) * 16 + r;
           if (v > best) { best = v; bidx = col; }
         }
 #pragma unroll
@@ -186,22 +250,25 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
           const int oi = __shfl_xor(bidx, o, 64);
           if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
         }
-        if (r == 0 && m < p.M) {
-          p.pval[(size_t)unit * p.M + m] = best;
-          p.pidx[(size_t)unit * p.M + m] = bidx;
+        if (r == 0 && mok) {
+          const unsigned long long key =
+              ((unsigned long long)ordered_bits(best) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)bidx);
+          __hip_atomic_fetch_max(p.amax + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       } else {
-        const bool mok = m < p.M;
         bf16_t* orow = p.out + (size_t)(mok ? m : 0) * p.ld_out;
         if constexpr (EPI == EPI_SWIGLU) {
-          const float g = rbf(acc[mt][0][i]);
-          const float u = rbf(acc[mt][1][i]);
-          const float s = rbf(g / (1.0f + expf(-g)));
-          if (mok) orow[unit * 16 + r] = f2bf(mul_rn(s, u));
+#pragma unroll
+          for (int j = 0; j < NTW / 2; ++j) {
+            const float g = rbf(acc[mt][2 * j][i]);
+            const float u = rbf(acc[mt][2 * j + 1][i]);
+            const float s = rbf(g / (1.0f + expf(-g)));
+            if (mok) orow[(unit * (NTW / 2) + j) * 16 + r] = f2bf(mul_rn(s, u));
+          }
         } else {
 #pragma unroll
           for (int nt = 0; nt < NTW; ++nt) {
-            const int col = (unit * NTW + nt) * 16 + r;
+            const long long col = (unit * NTW + nt) * 16 + r;
             if constexpr (EPI == EPI_RES) {
               const float rv = mok ? bf2f(p.res[(size_t)m * p.ld_out + col]) : 0.f;
               const bf16_t o = f2bf(add_rn(rv, rbf(acc[mt][nt][i])));
@@ -225,68 +292,268 @@ __global__ void __launch_bounds__(64 * KSPLIT) skinny_gemm_kernel(GemmParams p) 
   }
 }
 
-// Reduce the per-workgroup (max, index) partials of one row: lowest index wins ties.
-__global__ void __launch_bounds__(256) argmax_finalize_kernel(const float* __restrict__ pval,
-                                                               const int32_t* __restrict__ pidx, int units, int M,
-                                                               int64_t* __restrict__ out) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  const int m = blockIdx.x;
-  float best = -INFINITY;
-  int bidx = 0x7fffffff;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const float v = pval[(size_t)u * M + m];
-    const int i = pidx[(size_t)u * M + m];
-    if (v > best || (v == best && i < bidx)) { best = v; bidx = i; }
-  }
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bidx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      const float ov = sv[threadIdx.x + s];
-      const int oi = si[threadIdx.x + s];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
+// Cross-workgroup completion of one unit: store this workgroup's partial as
+// piece `slot` of `pieces` (device-coherent stores), count the arrival; the
+// last arriver sums the pieces in slot order (its own from registers), runs
+// the epilogue and re-arms the counter. Called by one whole wavefront.
+template <int MT, int NTW, int EPI>
+__device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int slot,
+                                             int pieces, int lane) {
+  f32x4_t* base = p.part + (size_t)unit * p.piece_stride * MT * NTW * 64 + lane;
+  f32x4_t* mine = base + (size_t)slot * MT * NTW * 64;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) store_dev(mine + (mt * NTW + nt) * 64, acc[mt][nt]);
+  __builtin_amdgcn_s_waitcnt(0);  // partial stores complete before the arrival is counted
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  unsigned old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(p.cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0, 64);
+  if (old != (unsigned)(pieces - 1)) return;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) {
+      f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < pieces; ++j)
+        s += (j == slot) ? acc[mt][nt] : load_dev(base + ((size_t)(j * MT + mt) * NTW + nt) * 64);
+      acc[mt][nt] = s;
     }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) out[m] = si[0];
+  if (lane == 0) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  epilogue<MT, NTW, EPI>(p, acc, unit, lane);
 }
 
-template <int MT, int NTW, int KSPLIT, bool NORM, int EPI>
-hipError_t launch(const GemmParams& p, int units, hipStream_t stream) {
-  skinny_gemm_kernel<MT, NTW, KSPLIT, NORM, EPI><<<units, 64 * KSPLIT, 0, stream>>>(p);
+template <int MT, int NTW, int WPG, bool NORM, int EPI>
+__global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
+  constexpr int U = 4 / NTW;  // k-steps per batch (4 KB of weights); two batches in flight per wavefront
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int KS = p.ks;
+  const int unit = blockIdx.x / KS;
+  const int ks = blockIdx.x - unit * KS;
+  const int KT = p.K >> 5;
+  const int nranges = KS * WPG;
+  const int kpw = (KT + nranges - 1) / nranges;
+  const int k0 = min(KT, (ks * WPG + wave) * kpw);
+  const int k1 = min(KT, k0 + kpw);
+
+  __shared__ f32x4_t red[WPG > 1 ? (WPG - 1) * MT * NTW * 64 : 1];
+
+  AOperand<MT, NORM> A;
+  A.init(p, r, q);
+  f32x4_t acc[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  accumulate<MT, NTW, U, NORM>(p, A, (size_t)unit, k0, k1, acc, r, q, lane, true);
+
+  // Wavefront partials -> wavefront 0, summed in wavefront order.
+  if constexpr (WPG > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) red[(((wave - 1) * MT + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt)
+        for (int w = 1; w < WPG; ++w) acc[mt][nt] += red[(((w - 1) * MT + mt) * NTW + nt) * 64 + lane];
+  }
+  if (KS > 1) {
+    finish_split<MT, NTW, EPI>(p, acc, unit, ks, KS, lane);   // split-K across workgroups
+  } else {
+    epilogue<MT, NTW, EPI>(p, acc, unit, lane);
+  }
+}
+
+// Stream-K decomposition: exactly one workgroup per CU (gridDim.x = CU count;
+// the LDS reservation keeps a second one off the CU). The units x K/32 weight
+// tiles, unit-major, are cut into gridDim.x equal contiguous ranges, so every
+// CU streams the same number of bytes; a CU's range is cut again into
+// SK_WAVES equal pieces, one per wavefront, each touching at most two units.
+// Units that lie entirely inside one CU's range are reduced through LDS (in
+// wavefront order) and finished there; a unit shared by several CUs is
+// finished by the last of them through finish_split (pieces in CU order), so
+// results do not depend on timing.
+constexpr int SK_WAVES = 8;
+constexpr int SK_PIECES = 4;                 // CUs that may share one unit
+constexpr int SK_LDS_BYTES = 96 * 1024;      // more than half of a CU's 160 KB
+
+__device__ __forceinline__ long long sk_begin(long long T, int G, long long c) { return T * c / G; }
+
+// CU whose range holds tile t.
+__device__ __forceinline__ long long sk_owner(long long t, long long T, int G) {
+  long long c = t * G / T;
+  while (c > 0 && sk_begin(T, G, c) > t) --c;
+  while (c + 1 < G && sk_begin(T, G, c + 1) <= t) ++c;
+  return c;
+}
+
+template <int MT, int NTW, bool NORM, int EPI>
+__global__ void __launch_bounds__(64 * SK_WAVES) sk_gemm_kernel(GemmParams p) {
+  constexpr int U = (MT == 1 ? 8 : 4) / NTW;
+  __shared__ f32x4_t red[SK_LDS_BYTES / 16];  // [wave][slot][mt][nt][lane]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const long long KT = p.K >> 5;
+  const long long units = p.N / (16 * NTW);
+  const long long T = units * KT;
+  const int G = gridDim.x;
+  const long long c = blockIdx.x;
+  const long long cs = sk_begin(T, G, c), ce = sk_begin(T, G, c + 1);
+  auto wave_begin = [&](int w) { return cs + (ce - cs) * w / SK_WAVES; };
+  const long long ws = wave_begin(wave), we = wave_begin(wave + 1);
+
+  AOperand<MT, NORM> A;
+  A.init(p, r, q);
+  const long long u0 = ws / KT;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const long long u = u0 + s;
+    const long long lo = max(ws, u * KT), hi = min(we, (u + 1) * KT);
+    f32x4_t acc[MT][NTW];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (lo < hi) accumulate<MT, NTW, U, NORM>(p, A, (size_t)u, (int)(lo - u * KT), (int)(hi - u * KT), acc, r, q, lane, s == 0);
+    else if (s == 0) A.stats(p, r, q);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) red[(((wave * 2 + s) * MT + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
+  }
+  __syncthreads();
+
+  // Units of this CU: wavefront j reduces units U0 + j, U0 + j + SK_WAVES, ...
+  if (ce <= cs) return;
+  const long long U0 = cs / KT, U1 = (ce - 1) / KT;
+  for (long long u = U0 + wave; u <= U1; u += SK_WAVES) {
+    f32x4_t acc[MT][NTW];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < SK_WAVES; ++w) {
+      const long long a = wave_begin(w), b = wave_begin(w + 1);
+      if (a >= b || b <= u * KT || a >= (u + 1) * KT) continue;  // wavefront w does not touch unit u
+      const int s = (int)(u - a / KT);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] += red[(((w * 2 + s) * MT + mt) * NTW + nt) * 64 + lane];
+    }
+    if (u * KT >= cs && (u + 1) * KT <= ce) {
+      epilogue<MT, NTW, EPI>(p, acc, u, lane);
+    } else {
+      const long long cf = sk_owner(u * KT, T, G), cl = sk_owner((u + 1) * KT - 1, T, G);
+      finish_split<MT, NTW, EPI>(p, acc, u, (int)(c - cf), (int)(cl - cf + 1), lane);
+    }
+  }
+}
+
+// token[m] = index held in a packed argmax key; the key is re-armed to zero.
+__global__ void __launch_bounds__(64) argmax_extract_kernel(unsigned long long* __restrict__ amax, int M,
+                                                            int64_t* __restrict__ out) {
+  const int m = blockIdx.x * 64 + threadIdx.x;
+  if (m >= M) return;
+  const unsigned long long key = amax[m];
+  out[m] = (int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+  amax[m] = 0ull;
+}
+
+template <int MT, int NTW, int WPG, bool NORM, int EPI>
+hipError_t launch(const GemmParams& p, int grid, hipStream_t stream) {
+  skinny_gemm_kernel<MT, NTW, WPG, NORM, EPI><<<grid, 64 * WPG, 0, stream>>>(p);
   return hipGetLastError();
 }
 
-// Dispatch over the instantiated (MT, NTW, KSPLIT) combinations.
+template <int MT, int NTW, bool NORM, int EPI>
+hipError_t launch_sk(const GemmParams& p, int grid, hipStream_t stream) {
+  sk_gemm_kernel<MT, NTW, NORM, EPI><<<grid, 64 * SK_WAVES, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
 template <bool NORM, int EPI>
-int dispatch(const GemmParams& p, int units, int mt, int ntw, int ksplit, hipStream_t stream) {
-#define QWEN_GEMM_CASE(MT_, NTW_, KS_) \
-  if (mt == MT_ && ntw == NTW_ && ksplit == KS_) return qwen_status(launch<MT_, NTW_, KS_, NORM, EPI>(p, units, stream));
-#define QWEN_GEMM_KS(MT_, NTW_) \
-  QWEN_GEMM_CASE(MT_, NTW_, 1) QWEN_GEMM_CASE(MT_, NTW_, 2) QWEN_GEMM_CASE(MT_, NTW_, 4) QWEN_GEMM_CASE(MT_, NTW_, 8)
+int dispatch_sk(const GemmParams& p, int grid, int mt, int ntw, hipStream_t stream) {
   if constexpr (EPI != EPI_SWIGLU) {
-    QWEN_GEMM_KS(1, 1)
-    QWEN_GEMM_CASE(1, 1, 16)
-    QWEN_GEMM_KS(2, 1)
+    if (mt == 1 && ntw == 1) return qwen_status(launch_sk<1, 1, NORM, EPI>(p, grid, stream));
+    if (mt == 2 && ntw == 1) return qwen_status(launch_sk<2, 1, NORM, EPI>(p, grid, stream));
   }
-  QWEN_GEMM_KS(1, 2)
-  QWEN_GEMM_KS(2, 2)
-#undef QWEN_GEMM_KS
+  if (mt == 1 && ntw == 2) return qwen_status(launch_sk<1, 2, NORM, EPI>(p, grid, stream));
+  if (mt == 2 && ntw == 2) return qwen_status(launch_sk<2, 2, NORM, EPI>(p, grid, stream));
+  return QWEN_EARG;
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Stream-K applies when every CU gets at least one tile, a unit spans at most
+// SK_PIECES CUs and a wavefront's share touches at most two units.
+bool sk_fits(int N, int K, int ntw, int G) {
+  if (G <= 0 || (ntw != 1 && ntw != 2)) return false;
+  const long long KT = K / 32, units = N / (16 * ntw), T = units * KT;
+  const long long lmin = T / G, lmax = (T + G - 1) / G;
+  if (lmin < 1) return false;
+  if ((KT - 1 + lmin - 1) / lmin + 1 > SK_PIECES) return false;
+  return (lmax + SK_WAVES - 1) / SK_WAVES <= KT;
+}
+
+// Dispatch over the instantiated (MT, NTW, WPG) launch shapes. Shapes whose
+// wavefront-reduction buffer would exceed 60 KB of LDS, or that would spill
+// registers, are not built (the call returns QWEN_EARG).
+template <bool NORM, int EPI>
+int dispatch(const GemmParams& p, int grid, int mt, int ntw, int wpg, hipStream_t stream) {
+#define QWEN_GEMM_CASE(MT_, NTW_, W_) \
+  if (mt == MT_ && ntw == NTW_ && wpg == W_) return qwen_status(launch<MT_, NTW_, W_, NORM, EPI>(p, grid, stream));
+#define QWEN_GEMM_W(MT_, NTW_) QWEN_GEMM_CASE(MT_, NTW_, 4) QWEN_GEMM_CASE(MT_, NTW_, 8)
+  if constexpr (EPI != EPI_SWIGLU) {
+    QWEN_GEMM_W(1, 1)
+    QWEN_GEMM_W(2, 1)
+  }
+  QWEN_GEMM_W(1, 2)
+  QWEN_GEMM_W(2, 2)
+  QWEN_GEMM_W(1, 4)
+  QWEN_GEMM_W(2, 4)
+  if constexpr (!NORM) {  // 16 wavefronts (128 VGPRs each) fit only without the norm prologue
+    QWEN_GEMM_CASE(1, 1, 16)
+    QWEN_GEMM_CASE(1, 2, 16)
+    QWEN_GEMM_CASE(2, 2, 16)
+  }
+#undef QWEN_GEMM_W
 #undef QWEN_GEMM_CASE
   return QWEN_EARG;
 }
 
-int check_common(const void* x, const void* w, int M, int N, int K, int ntw, int ksplit) {
+int check_shape(const void* x, const void* w, int M, int N, int K, int ntw, int wpg, int ks) {
   if (!x || !w) return QWEN_ENULL;
   if (M <= 0 || M > 32 || N <= 0 || K <= 0 || K % 32 != 0) return QWEN_EARG;
-  if (ntw != 1 && ntw != 2) return QWEN_EARG;
-  if (ksplit != 1 && ksplit != 2 && ksplit != 4 && ksplit != 8 && ksplit != 16) return QWEN_EARG;
+  if (ntw != 1 && ntw != 2 && ntw != 4) return QWEN_EARG;
+  if (wpg != 4 && wpg != 8 && wpg != 16) return QWEN_EARG;
+  if (ntw == 4 && wpg == 16) return QWEN_EARG;
+  if (ks == 0) return (wpg == SK_WAVES && ntw <= 2) ? QWEN_OK : QWEN_EARG;  // stream-K
+  if (ks < 1 || ks > 64 || ks * wpg > K / 32) return QWEN_EARG;  // every wavefront owns >= 1 k-step
   if (N % (16 * ntw) != 0) return QWEN_EARG;
+  if ((long long)(N / (16 * ntw)) * ks > 0x7fffffffLL) return QWEN_EARG;
   return QWEN_OK;
 }
 
@@ -294,57 +561,86 @@ int check_common(const void* x, const void* w, int M, int N, int K, int ntw, int
 
 extern "C" {
 
+long long qwen_linear_workspace_bytes(int M, int N, int ntw, int ks) {
+  if (M <= 0 || M > 32 || N <= 0 || (ntw != 1 && ntw != 2 && ntw != 4) || ks < 0 || N % (16 * ntw) != 0) return 0;
+  if (ks == 1) return 0;
+  const long long units = N / (16 * ntw);
+  const long long mt = M > 16 ? 2 : 1;
+  const long long pieces = ks == 0 ? SK_PIECES : ks;  // ks == 0: stream-K
+  // A fixed counter region first (so GEMMs of any shape can share one
+  // workspace without their partials landing on each other's counters),
+  // then the partials.
+  return QWEN_LINEAR_COUNTER_BYTES + units * pieces * mt * ntw * 64 * 16;
+}
+
 // epi: 0 = store, 1 = residual add (residual may alias out), 2 = SwiGLU pair
 // (N counts gate + up rows; out has N/2 columns). norm_w == nullptr: no norm prologue.
 int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* norm_w,
-                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int ksplit,
-                hipStream_t stream) {
-  int st = check_common(x, w_tiled, M, N, K, ntw, ksplit);
+                const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int wpg,
+                int ks, void* workspace, long long workspace_bytes, hipStream_t stream) {
+  int st = check_shape(x, w_tiled, M, N, K, ntw, wpg, ks);
   if (st) return st;
   if (!out) return QWEN_ENULL;
   if (epi == EPI_RES && !residual) return QWEN_ENULL;
   if (norm_w && !psq_in) return QWEN_ENULL;
   if (psq_out && (epi != EPI_RES || N % 16 != 0)) return QWEN_EARG;
-  if (epi == EPI_SWIGLU && ntw != 2) return QWEN_EARG;
+  if (epi == EPI_SWIGLU && ntw < 2) return QWEN_EARG;
   if (epi < EPI_STORE || epi > EPI_SWIGLU) return QWEN_EARG;
   const int out_cols = epi == EPI_SWIGLU ? N / 2 : N;
   if (ld_out < out_cols) return QWEN_EARG;
-  GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, (const bf16_t*)residual,
-               (bf16_t*)out, nullptr, nullptr, psq_in, psq_out, M, N, K, ld_out, eps};
+  const long long need = qwen_linear_workspace_bytes(M, N, ntw, ks);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return workspace ? QWEN_EWORKSPACE : QWEN_ENULL;
   const int units = N / (16 * ntw);
   const int mt = M > 16 ? 2 : 1;
+  if (units > QWEN_LINEAR_COUNTER_BYTES / 4) return QWEN_EARG;
+  const bool split = ks != 1;
+  unsigned* cnt = split ? (unsigned*)workspace : nullptr;
+  f32x4_t* part = split ? (f32x4_t*)((char*)workspace + QWEN_LINEAR_COUNTER_BYTES) : nullptr;
+  GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, (const bf16_t*)residual,
+               (bf16_t*)out, nullptr, psq_in, psq_out, part, cnt, M, N, K, ld_out, ks, ks == 0 ? SK_PIECES : ks, eps};
+  if (ks == 0) {  // stream-K: one workgroup per CU
+    const int G = cu_count();
+    if (!sk_fits(N, K, ntw, G)) return QWEN_EARG;
+    if (epi == EPI_STORE) return norm_w ? dispatch_sk<true, EPI_STORE>(p, G, mt, ntw, stream)
+                                        : dispatch_sk<false, EPI_STORE>(p, G, mt, ntw, stream);
+    if (epi == EPI_RES) return norm_w ? QWEN_EARG : dispatch_sk<false, EPI_RES>(p, G, mt, ntw, stream);
+    return norm_w ? dispatch_sk<true, EPI_SWIGLU>(p, G, mt, ntw, stream) : QWEN_EARG;
+  }
+  const int grid = units * ks;
   // Instantiated variants: norm+store (QKV), store (plain linear), residual
   // (O / down projections), norm+SwiGLU (gate/up).
-  if (epi == EPI_STORE) return norm_w ? dispatch<true, EPI_STORE>(p, units, mt, ntw, ksplit, stream)
-                                      : dispatch<false, EPI_STORE>(p, units, mt, ntw, ksplit, stream);
-  if (epi == EPI_RES) return norm_w ? QWEN_EARG : dispatch<false, EPI_RES>(p, units, mt, ntw, ksplit, stream);
-  return norm_w ? dispatch<true, EPI_SWIGLU>(p, units, mt, ntw, ksplit, stream) : QWEN_EARG;
+  if (epi == EPI_STORE) return norm_w ? dispatch<true, EPI_STORE>(p, grid, mt, ntw, wpg, stream)
+                                      : dispatch<false, EPI_STORE>(p, grid, mt, ntw, wpg, stream);
+  if (epi == EPI_RES) return norm_w ? QWEN_EARG : dispatch<false, EPI_RES>(p, grid, mt, ntw, wpg, stream);
+  return norm_w ? dispatch<true, EPI_SWIGLU>(p, grid, mt, ntw, wpg, stream) : QWEN_EARG;
 }
 
-long long qwen_argmax_workspace_bytes(int M, int N, int ntw) {
-  if (M <= 0 || N <= 0 || (ntw != 1 && ntw != 2)) return 0;
-  const long long units = N / (16 * ntw);
-  return units * M * (long long)(sizeof(float) + sizeof(int32_t));
-}
-
-// Final RMSNorm (norm_w) + LM head GEMM + argmax over the bf16 logits,
-// lowest index on ties. out_tok: [M] int64.
+// Final RMSNorm (norm_w) + LM head GEMM + argmax over the bf16 logits, lowest
+// index on ties. amax: [M] packed keys that must be zero before the call (the
+// consumer, qwen_argmax_extract or qwen_decode_finish, re-arms them).
+// With out_tok != nullptr the tokens are also extracted here (second kernel).
 int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, float eps, const void* w_tiled, int M,
-                        int N, int K, void* workspace, long long workspace_bytes, int64_t* out_tok, int ntw,
-                        int ksplit, hipStream_t stream) {
-  int st = check_common(x, w_tiled, M, N, K, ntw, ksplit);
+                        int N, int K, unsigned long long* amax, int64_t* out_tok, int ntw, int wpg,
+                        hipStream_t stream) {
+  int st = check_shape(x, w_tiled, M, N, K, ntw, wpg, 1);
   if (st) return st;
-  if (!out_tok || !workspace || !norm_w || !psq_in) return QWEN_ENULL;
-  if (workspace_bytes < qwen_argmax_workspace_bytes(M, N, ntw)) return QWEN_EWORKSPACE;
+  if (!amax || !norm_w || !psq_in) return QWEN_ENULL;
   const int units = N / (16 * ntw);
-  float* pval = (float*)workspace;
-  int32_t* pidx = (int32_t*)(pval + (size_t)units * M);
-  GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, nullptr, nullptr, pval, pidx,
-               psq_in, nullptr, M, N, K, 0, eps};
+  GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, nullptr, nullptr, amax, psq_in,
+               nullptr, nullptr, nullptr, M, N, K, 0, 1, 1, eps};
   const int mt = M > 16 ? 2 : 1;
-  st = dispatch<true, EPI_ARGMAX>(p, units, mt, ntw, ksplit, stream);
-  if (st) return st;
-  argmax_finalize_kernel<<<M, 256, 0, stream>>>(pval, pidx, units, M, out_tok);
+  st = dispatch<true, EPI_ARGMAX>(p, units, mt, ntw, wpg, stream);
+  if (st || !out_tok) return st;
+  argmax_extract_kernel<<<(M + 63) / 64, 64, 0, stream>>>(amax, M, out_tok);
+  QWEN_RETURN_LAUNCH();
+}
+
+// out[m] = token index of amax[m]; re-arms amax[m] to zero.
+int qwen_argmax_extract(unsigned long long* amax, int M, int64_t* out, hipStream_t stream) {
+  if (!amax || !out) return QWEN_ENULL;
+  if (M < 0) return QWEN_EARG;
+  if (M == 0) return QWEN_OK;
+  argmax_extract_kernel<<<(M + 63) / 64, 64, 0, stream>>>(amax, M, out);
   QWEN_RETURN_LAUNCH();
 }
 

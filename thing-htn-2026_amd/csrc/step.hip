@@ -1,33 +1,73 @@
 // Per-step token bookkeeping on the device (no host synchronisation).
 //
-// Restates engine/engine.py:941-953 (_plain_step after the model step): the
-// greedy token of sequence b goes to hist[b, pos[b] + 1] and pos[b] advances,
-// unless the sequence already produced its max_new_tokens (frozen rows write
-// to the dump slot and keep their position).
+// Restates the tail of engine/engine.py:941-953 (_plain_step after the model
+// step) and the head of the next step (engine/engine.py:1101, the embedding of
+// hist[pos]), fused into one launch that follows the LM head:
+//   token[b]   = index held in the packed argmax key amax[b] (re-armed to zero)
+//   hist[b, pos[b] + 1] = token[b] and pos[b] += 1, unless the sequence already
+//   produced its max_new_tokens (frozen rows write to the dump slot cap-1 and
+//   keep their position)
+//   h[b, :]    = embedding row of hist[b, pos[b]] (the next step's input) and
+//   psq[b, :]  = its per-16-column sums of squares (the next RMSNorm's statistics).
 #include "common.h"
 
 namespace {
 
-__global__ void plain_update_kernel(const int64_t* __restrict__ next, int64_t* __restrict__ hist,
-                                    int32_t* __restrict__ pos, const int64_t* __restrict__ s_buf,
-                                    const int64_t* __restrict__ ntarget, int B, int cap) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= B) return;
-  const long long L = (long long)pos[b] + 1;
+constexpr int FIN_THREADS = 256;
+
+__global__ void __launch_bounds__(FIN_THREADS) decode_finish_kernel(
+    unsigned long long* __restrict__ amax, int64_t* __restrict__ next, int64_t* __restrict__ hist,
+    int32_t* __restrict__ pos, const int64_t* __restrict__ s_buf, const int64_t* __restrict__ ntarget,
+    const bf16_t* __restrict__ w, bf16_t* __restrict__ h, float* __restrict__ psq, int cap, long long V, int K) {
+  const int b = blockIdx.x;
+  // Every thread reads the state before thread 0 updates it.
+  const unsigned long long key = amax[b];
+  const int64_t tok = (int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+  const long long p0 = pos[b];
+  const long long L = p0 + 1;
   const bool done = (L - s_buf[0]) >= ntarget[0];
-  long long idx = done ? (long long)(cap - 1) : L;
-  idx = idx < 0 ? 0 : (idx >= cap ? cap - 1 : idx);
-  hist[(long long)b * cap + idx] = next[b];
-  if (!done) pos[b] += 1;
+  const long long pc = p0 < 0 ? 0 : (p0 >= cap ? cap - 1 : p0);
+  long long id = done ? hist[(long long)b * cap + pc] : tok;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long idx = done ? (long long)(cap - 1) : L;
+    idx = idx < 0 ? 0 : (idx >= cap ? cap - 1 : idx);
+    hist[(long long)b * cap + idx] = tok;
+    if (!done) pos[b] = (int32_t)L;
+    next[b] = tok;
+    amax[b] = 0ull;
+  }
+  // Embedding gather from the tiled table (ids clamped into [0, V)).
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+  const long long KT = K / 32;
+  const long long nt = id >> 4;
+  const int r = (int)(id & 15);
+  const int kc = K / 8;
+  for (int c0 = 0; c0 < kc; c0 += FIN_THREADS) {
+    const int cl = c0 + threadIdx.x;
+    const bool live = cl < kc;
+    const int chunk = live ? cl : 0;  // dead lanes redo chunk 0 so the pair shuffle stays uniform
+    const int kt = chunk >> 2, q = chunk & 3;
+    const uint4 v = reinterpret_cast<const uint4*>(w)[(nt * KT + kt) * 64 + q * 16 + r];
+    if (live) reinterpret_cast<uint4*>(h + (long long)b * K)[chunk] = v;
+    float f[8], s = 0.f;
+    unpack8(v, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
+    s += __shfl_xor(s, 1, 64);
+    if (live && (chunk & 1) == 0) psq[(long long)b * (K / 16) + (chunk >> 1)] = s;
+  }
 }
 
 }  // namespace
 
-extern "C" int qwen_plain_update(const int64_t* next, int64_t* hist, int32_t* pos, const int64_t* s_buf,
-                                 const int64_t* ntarget, int B, int cap, hipStream_t stream) {
-  if (!next || !hist || !pos || !s_buf || !ntarget) return QWEN_ENULL;
-  if (B < 0 || cap <= 0) return QWEN_EARG;
+extern "C" int qwen_decode_finish(unsigned long long* amax, int64_t* next, int64_t* hist, int32_t* pos,
+                                  const int64_t* s_buf, const int64_t* ntarget, const void* w_tiled, void* h,
+                                  float* psq, int B, int cap, long long V, int K, hipStream_t stream) {
+  if (!amax || !next || !hist || !pos || !s_buf || !ntarget || !w_tiled || !h || !psq) return QWEN_ENULL;
+  if (B < 0 || cap <= 0 || V <= 0 || V % 16 != 0 || K <= 0 || K % 32 != 0) return QWEN_EARG;
   if (B == 0) return QWEN_OK;
-  plain_update_kernel<<<(B + 63) / 64, 64, 0, stream>>>(next, hist, pos, s_buf, ntarget, B, cap);
+  decode_finish_kernel<<<B, FIN_THREADS, 0, stream>>>(amax, next, hist, pos, s_buf, ntarget, (const bf16_t*)w_tiled,
+                                                      (bf16_t*)h, psq, cap, V, K);
   QWEN_RETURN_LAUNCH();
 }

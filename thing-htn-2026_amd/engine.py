@@ -11,13 +11,12 @@ Per decode step the device runs only hand-written HIP kernels from
 ``qwen_hip`` (libqwen_hip.so), recorded once per batch shape into one HIP
 graph (``torch.cuda.CUDAGraph``) and replayed per token:
 
-    embed(hist[pos])                                   1 kernel
-    36 x [ norm+QKV GEMM | QK-norm+RoPE+KV write |
-           split-K attention (partial + merge) |
+    36 x [ norm+QKV GEMM |
+           QK-norm + RoPE + KV write + split-K attention + merge |
            O GEMM + residual | norm+gate/up GEMM+SwiGLU |
-           down GEMM + residual ]                      7 kernels / layer
-    final norm + LM head + argmax                      2 kernels
-    history / position update                          1 kernel
+           down GEMM + residual ]                      5 kernels / layer
+    final norm + LM head + argmax                      1 kernel
+    token / history / position update + next embedding 1 kernel
 
 Torch is used for device memory, the KV cache, the RoPE tables, graph
 capture, host<->device copies and (for now) the prompt forward's large GEMMs
@@ -259,26 +258,30 @@ class Engine:
         key = (B, T)
         if key not in self.bufs:
             M, dev = B * T, self.device
-            S = ops.choose_num_splits(B, self.Nkv, self.CAP)
-            lm_cfg = ops.lm_head_config(M, self.V, self.H)
+            S = ops.choose_num_splits(B, self.Nkv, self.CAP, T)
+            W_qkv = (self.Nq + 2 * self.Nkv) * self.D
+            cfg = {
+                "qkv": ops.gemm_config(M, W_qkv, self.H),
+                "o": ops.gemm_config(M, self.H, self.Nq * self.D),
+                "gu": ops.gemm_config(M, 2 * self.I, self.H, True),
+                "down": ops.gemm_config(M, self.H, self.I),
+            }
+            n_of = {"qkv": W_qkv, "o": self.H, "gu": 2 * self.I, "down": self.H}
+            ws = max(ops.linear_workspace_bytes(M, n_of[k], c[0], c[2]) for k, c in cfg.items())
             self.bufs[key] = {
-                "h": torch.empty((M, self.H), dtype=BF16, device=dev),
-                "qkv": torch.empty((M, (self.Nq + 2 * self.Nkv) * self.D), dtype=BF16, device=dev),
-                "q": torch.empty((B, T, self.Nq, self.D), dtype=BF16, device=dev),
+                "h": torch.zeros((M, self.H), dtype=BF16, device=dev),
+                "qkv": torch.empty((M, W_qkv), dtype=BF16, device=dev),
                 "a": torch.empty((B, T, self.Nq * self.D), dtype=BF16, device=dev),
                 "p": torch.empty((M, self.I), dtype=BF16, device=dev),
-                "psq": torch.empty((M, self.H // 16), dtype=torch.float32, device=dev),
+                "psq": torch.zeros((M, self.H // 16), dtype=torch.float32, device=dev),
                 "next": torch.empty((M,), dtype=torch.int64, device=dev),
+                "keys": ops.argmax_keys(M, dev),
                 "splits": S,
-                "attn_ws": torch.empty(max(4, ops.attn_workspace_bytes(B, T, self.Nq, self.Nkv, self.D, S)),
-                                       dtype=torch.uint8, device=dev),
-                "lm_cfg": lm_cfg,
-                "cfg_qkv": ops.gemm_config(M, (self.Nq + 2 * self.Nkv) * self.D, self.H),
-                "cfg_o": ops.gemm_config(M, self.H, self.Nq * self.D),
-                "cfg_gu": ops.gemm_config(M, 2 * self.I, self.H, True),
-                "cfg_down": ops.gemm_config(M, self.H, self.I),
-                "lm_ws": torch.empty(ops.argmax_workspace_bytes(M, self.V, lm_cfg[0]), dtype=torch.uint8,
-                                     device=dev),
+                "attn_waves": ops.attn_waves(B, T),
+                "attn_ws": ops.attn_workspace(B, T, self.Nq, self.Nkv, self.D, S, dev),
+                "gemm_ws": ops.linear_workspace(ws, dev),
+                "cfg": cfg,
+                "lm_cfg": ops.lm_head_config(M, self.V, self.H),
             }
         return self.bufs[key]
 
@@ -286,45 +289,54 @@ class Engine:
     def _step(self, T, tok=None, hidden=None):
         """One decode step of ``T`` tokens per sequence (``engine/engine.py:1093-1121``).
 
-        Token ids come from ``hist[b, pos[b]]`` (T = 1, the plain step) or from
-        ``tok [B, T]`` int64. Positions are ``pos_buf``; K/V are written at
-        ``pos + t``. Returns the greedy ``next [B*T]`` int64 buffer. Issues only
+        With ``tok [B, T]`` int64 the step embeds those ids and returns the
+        greedy ``next [B*T]`` int64 buffer. Without it (T = 1, the plain step)
+        the input rows are already in ``h`` / ``psq`` (the embedding of
+        ``hist[b, pos[b]]``, left there by the previous step's tail or by
+        ``_prime``) and the argmax stays in the packed keys for ``decode_finish``.
+        Positions are ``pos_buf``; K/V are written at ``pos + t``. Issues only
         HIP kernels and allocates nothing, so it is capturable.
         """
         B = self.B
         M = B * T
         b = self._buffers(B, T)
-        h, qkv, q, a, p, psq = b["h"], b["qkv"], b["q"], b["a"], b["p"], b["psq"]
+        h, qkv, a, p, psq, cfg, ws = b["h"], b["qkv"], b["a"], b["p"], b["psq"], b["cfg"], b["gemm_ws"]
         # psq holds the per-16-column sums of squares of the current residual
         # stream h: written by whoever last wrote h (embedding, O / down
         # epilogues), read by the next normed projection.
-        if tok is None:
-            assert T == 1
-            ops.embed_hist(self.hist_buf, self.pos_buf, self.embed, h, psq_out=psq)
-        else:
+        if tok is not None:
             ops.embed(tok.reshape(-1), self.embed, out=h, psq_out=psq)
+        else:
+            assert T == 1
         for l, w in enumerate(self.layers):
-            ops.fused_linear(h, w.w_qkv, b["cfg_qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq)
-            ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
-                                   self.k_cache[l], self.v_cache[l], out=q)
-            ops.attn_decode(q, self.k_cache[l], self.v_cache[l], self.pos_buf, self.scale, b["splits"], len_add=T,
-                            out=a, workspace=b["attn_ws"])
-            ops.fused_linear(a.view(M, -1), w.w_o, b["cfg_o"], residual=h, out=h, psq_out=psq)
-            ops.fused_linear(h, w.w_gu, b["cfg_gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, psq_in=psq)
-            ops.fused_linear(p, w.w_down, b["cfg_down"], residual=h, out=h, psq_out=psq)
+            ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq, workspace=ws)
+            ops.attn_decode_fused(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
+                                  self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
+                                  workspace=b["attn_ws"], waves=b["attn_waves"])
+            ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
+            ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, psq_in=psq,
+                             workspace=ws)
+            ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
             if hidden is not None:
                 hidden.append(h.clone())
-        ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"], out=b["next"],
-                           workspace=b["lm_ws"], psq_in=psq)
+        extract = tok is not None
+        ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"], out=b["next"] if extract else None,
+                           keys=b["keys"], psq_in=psq, extract=extract)
         return b["next"]
 
     def _plain_step(self):
-        """``_plain_step`` (``engine/engine.py:941-953``): read hist[pos], step, write hist[pos+1], pos += 1."""
-        nxt = self._step(1)
-        ops._lib.call("qwen_plain_update", nxt.data_ptr(), self.hist_buf.data_ptr(), self.pos_buf.data_ptr(),
-                      self.s_buf.data_ptr(), self.ntarget_buf.data_ptr(), self.B, self.CAP,
-                      torch.cuda.current_stream().cuda_stream)
-        return nxt
+        """``_plain_step`` (``engine/engine.py:941-953``): step on hist[pos], write hist[pos+1], pos += 1,
+        and leave the embedding of the new hist[pos] in ``h`` for the next step."""
+        self._step(1)
+        b = self._buffers(self.B, 1)
+        ops.decode_finish(b["keys"], b["next"], self.hist_buf, self.pos_buf, self.s_buf, self.ntarget_buf, self.embed,
+                          b["h"], b["psq"])
+        return b["next"]
+
+    def _prime(self):
+        """Embed ``hist[b, pos[b]]`` into the plain step's input rows (before the first decode step)."""
+        b = self._buffers(self.B, 1)
+        ops.embed_hist(self.hist_buf, self.pos_buf, self.embed, b["h"], psq_out=b["psq"])
 
     def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
         """Greedy next token at every position of ``tok [B, T]`` (the speculative verify forward
@@ -485,6 +497,7 @@ class Engine:
             self.pos_buf.fill_(S)
             self.s_buf.fill_(S)
             self.ntarget_buf.fill_(N)
+            self._prime()
             yield from self._decode_loop(first, B, N)
 
     def _decode_loop(self, first, B, N):

@@ -25,13 +25,16 @@ SIGNATURES = {
     "qwen_silu_mul": (_i, [_p, _p, _i, _i, _p]),
     "qwen_qk_norm_rope_cache": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _p]),
     "qwen_attn_workspace_bytes": (_ll, [_i, _i, _i, _i, _i, _i]),
-    "qwen_attn_decode": (_i, [_p, _p, _p, _p, _i, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "qwen_attn_decode": (_i, [_p, _p, _p, _p, _i, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p]),
+    "qwen_attn_decode_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _i, _f,
+                                    _f, _i, _i, _p]),
     "qwen_sumsq16": (_i, [_p, _p, _i, _i, _p]),
-    "qwen_linear": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _p]),
-    "qwen_argmax_workspace_bytes": (_ll, [_i, _i, _i]),
-    "qwen_lm_head_argmax": (_i, [_p, _p, _p, _f, _p, _i, _i, _i, _p, _ll, _p, _i, _i, _p]),
+    "qwen_linear_workspace_bytes": (_ll, [_i, _i, _i, _i]),
+    "qwen_linear": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _i, _p, _ll, _p]),
+    "qwen_lm_head_argmax": (_i, [_p, _p, _p, _f, _p, _i, _i, _i, _p, _p, _i, _i, _p]),
+    "qwen_argmax_extract": (_i, [_p, _i, _p, _p]),
     "qwen_embed": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _ll, _i, _p]),
-    "qwen_plain_update": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "qwen_decode_finish": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _ll, _i, _p]),
     "qwen_tile_weight": (_i, [_p, _p, _ll, _i, _i, _p]),
     "qwen_init_weight": (_i, [_p, _ll, _i, _i, _i, _pi, _pi, _i, ctypes.c_ulonglong, _f, _p]),
 }

@@ -106,27 +106,44 @@ def qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions
 
 # --------------------------------------------------------------- attention
 
-def choose_num_splits(B: int, Nkv: int, cap: int) -> int:
-    """Context splits per (sequence, KV head) for a decode shape.
+def choose_num_splits(B: int, Nkv: int, cap: int, T: int = 1) -> int:
+    """Context splits per (sequence, KV head, query) for a decode shape.
 
-    Targets about 2048 workgroups (8 per CU on 256 CUs) while keeping at least
-    64 cache slots per split; power of two in [1, 64]. Fixed per captured graph,
-    as in the reference (``attention.py:94-110``), where the target was 264.
+    Targets about 256 workgroups (one per CU) while keeping at least 128 cache
+    slots per split; power of two in [1, 64]. Fixed per captured graph, as in
+    the reference (``attention.py:94-110``), where the target was 264 programs.
     """
-    want = max(1, math.ceil(2048 / max(1, B * Nkv)))
-    limit = max(1, cap // 64)
+    want = max(1, math.ceil(256 / max(1, B * Nkv * T)))
+    limit = max(1, cap // 128)
     s = 1
     while s * 2 <= min(want, limit, 64):
         s *= 2
     return s
 
 
+def attn_waves(B: int, T: int) -> int:
+    """Wavefronts per attention workgroup (measured): 4 for latency-bound small batches,
+    8 once the context stream dominates."""
+    return 8 if B * T >= 8 and T == 1 else 4
+
+
+ATTN_WAVES = 8   # wavefronts per attention workgroup
+
+
 def attn_workspace_bytes(B, T, Nq, Nkv, D, num_splits) -> int:
     return _lib.query("qwen_attn_workspace_bytes", B, T, Nq, Nkv, D, num_splits)
 
 
+def attn_workspace(B, T, Nq, Nkv, D, num_splits, device) -> torch.Tensor:
+    """Zeroed workspace for ``num_splits > 1`` (split partials + arrival counters that
+    every launch re-arms to zero, so one allocation serves any number of launches)."""
+    return torch.zeros(max(16, attn_workspace_bytes(B, T, Nq, Nkv, D, num_splits)), dtype=torch.uint8,
+                       device=device)
+
+
 def attn_decode(q, k_cache, v_cache, lengths, scale, num_splits, *, len_add: int = 0,
-                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                waves: int = ATTN_WAVES) -> torch.Tensor:
     """Causal decode attention of ``T`` new queries over the cache (``attention.py:278-348``).
 
     ``lengths [B]`` int32 counts valid slots including the ``T`` new ones
@@ -143,13 +160,47 @@ def attn_decode(q, k_cache, v_cache, lengths, scale, num_splits, *, len_add: int
     S = int(num_splits)
     assert S >= 1
     q = q.contiguous()
-    need = attn_workspace_bytes(B, T, Nq, Nkv, D, S)
     if workspace is None:
-        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+        workspace = attn_workspace(B, T, Nq, Nkv, D, S, q.device)
     o = out if out is not None else torch.empty((B, T, Nq * D), dtype=BF16, device=q.device)
     _lib.call("qwen_attn_decode", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), lengths.data_ptr(),
               int(len_add), o.data_ptr(), workspace.data_ptr(), workspace.numel(), B, T, Nq, Nkv, D, CAP,
-              float(scale), S, _stream())
+              float(scale), S, int(waves), _stream())
+    return o
+
+
+def attn_decode_fused(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, T, k_cache, v_cache, scale,
+                      num_splits, *, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                      waves: int = ATTN_WAVES) -> torch.Tensor:
+    """``qk_norm_rope_cache`` followed by ``attn_decode`` in one launch (decode step).
+
+    Same arguments and effects as the two reference ops in sequence
+    (``rope.py:169-226``, ``attention.py:278-348``): K/V of tokens
+    ``positions[b] + t`` are written to the caches, and the attention output of
+    the T new queries (lengths ``positions + T``) is returned as ``[B, T, Nq*D]``.
+    """
+    _gpu(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache)
+    B, Nkv, CAP, D = k_cache.shape
+    M, W = qkv.shape
+    assert D == 128 and W % D == 0 and W // D > 2 * Nkv, f"qkv width {W} vs {Nkv} KV heads of {D}"
+    Nq = W // D - 2 * Nkv
+    assert Nq == 4 * Nkv and M == B * T and 1 <= T <= 16, "G = 4, rows = B*T, T <= 16"
+    assert qkv.dtype == BF16 and qkv.is_contiguous()
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and v_cache.shape == k_cache.shape
+    assert k_cache.dtype == BF16 and v_cache.dtype == BF16
+    assert q_norm_w.numel() == D and k_norm_w.numel() == D and q_norm_w.is_contiguous() and k_norm_w.is_contiguous()
+    assert cos_tab.dim() == 2 and cos_tab.shape[1] == D and cos_tab.is_contiguous() and sin_tab.shape == cos_tab.shape
+    assert cos_tab.dtype == BF16 and sin_tab.dtype == BF16
+    assert positions.dtype == torch.int32 and positions.numel() == B and positions.is_contiguous()
+    S = int(num_splits)
+    assert S >= 1
+    if workspace is None:
+        workspace = attn_workspace(B, T, Nq, Nkv, D, S, qkv.device)
+    o = out if out is not None else torch.empty((B, T, Nq * D), dtype=BF16, device=qkv.device)
+    _lib.call("qwen_attn_decode_fused", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+              cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              o.data_ptr(), workspace.data_ptr(), workspace.numel(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0],
+              float(eps), float(scale), S, int(waves), _stream())
     return o
 
 
@@ -206,35 +257,48 @@ def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
     return t
 
 
-# Measured launch shapes (ntw, ksplit) for the Qwen3-4B projections on MI355X,
-# keyed by (N, K, SwiGLU pair) and by M <= 16 (one A fragment) or M <= 32 (two).
+# Measured launch shapes (ntw, waves, ksplit) for the Qwen3-4B projections on
+# MI355X (graph-replayed, 36 weight copies rotated), keyed by (N, K, SwiGLU
+# pair) and by M == 1, M <= 16 (one A fragment) or M <= 32 (two).
 _TUNED = {
-    (6144, 2560, False): {16: (1, 4), 32: (2, 4)},     # QKV
-    (2560, 4096, False): {16: (1, 16), 32: (1, 8)},    # O
-    (19456, 2560, True): {16: (2, 2), 32: (2, 2)},     # gate/up + SwiGLU
-    (2560, 9728, False): {16: (1, 16), 32: (1, 8)},    # down
+    (6144, 2560, False): {1: (2, 8, 1), 16: (2, 8, 1), 32: (2, 4, 1)},      # QKV
+    (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 32: (1, 4, 1)},      # O
+    (19456, 2560, True): {1: (2, 8, 1), 16: (2, 4, 1), 32: (4, 4, 1)},      # gate/up + SwiGLU
+    (2560, 9728, False): {1: (1, 16, 1), 16: (1, 8, 1), 32: (2, 4, 2)},     # down
 }
 
 
-def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, int]:
-    """(ntw, ksplit) launch shape for ``x[M, K] @ W[N, K]^T``.
+def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, int, int]:
+    """(ntw, waves, ksplit) launch shape for ``x[M, K] @ W[N, K]^T``.
 
-    Known Qwen3-4B shapes use the measured table; otherwise: enough wavefronts
-    to cover 256 CUs (about 2048), at least 8 k-steps (8 KB of weight per
+    ``ksplit == 0`` selects the stream-K launch (one workgroup of 8 wavefronts
+    per CU, equal weight bytes per CU). Known Qwen3-4B shapes use the measured
+    table; otherwise: 8 wavefronts per
+    workgroup and enough workgroups (n-tile groups x k-splits) to give about
+    four per CU on 256 CUs, keeping at least 4 k-steps (4 KB of weight per
     n-tile) per wavefront.
     """
     tuned = _TUNED.get((N, K, bool(silu_pair)))
     if tuned is not None:
-        return tuned[16 if M <= 16 else 32]
+        return tuned[1 if M == 1 else (16 if M <= 16 else 32)]
     ntw = 2 if silu_pair else 1
+    waves = 8 if K // 32 >= 32 else 4
     units = N // (16 * ntw)
     KT = K // 32
     ks = 1
-    while ks < 16 and units * ks < 2048 and KT // (ks * 2) >= 8:
+    while ks < 64 and units * ks < 1024 and KT // (ks * 2 * waves) >= 4:
         ks *= 2
-    if (ntw == 2 or M > 16) and ks > 8:   # 16-wavefront variants exist for one n-tile, one m-tile
-        ks = 8
-    return ntw, ks
+    return ntw, waves, ks
+
+
+def linear_workspace_bytes(M: int, N: int, ntw: int, ks: int) -> int:
+    return _lib.query("qwen_linear_workspace_bytes", M, N, ntw, ks)
+
+
+def linear_workspace(nbytes: int, device) -> torch.Tensor:
+    """Zeroed split-K workspace (partials + arrival counters; every launch re-arms the
+    counters, so one allocation serves any sequence of launches on one stream)."""
+    return torch.zeros(max(256, int(nbytes)), dtype=torch.uint8, device=device)
 
 
 def sumsq16(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -250,17 +314,18 @@ def sumsq16(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 
 def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps: float = 0.0, residual=None,
                  silu_pair: bool = False, out: torch.Tensor | None = None, psq_in: torch.Tensor | None = None,
-                 psq_out: torch.Tensor | None = None) -> torch.Tensor:
+                 psq_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``x @ w.T`` with optional RMSNorm prologue and residual / SwiGLU epilogue (``gemm_fused.py:136-173``).
 
     ``x [M <= 32, K]`` bf16; ``w`` tiled ``[N, K]`` (for ``silu_pair`` a pair-
     interleaved ``cat(gate, up)`` and the output is ``[M, N/2]``); ``norm_w [K]``;
     ``residual [M, N]`` (may be the same tensor as ``out``). ``cfg`` is
-    ``(ntw, ksplit)`` or ``None`` for ``gemm_config``. ``psq_in`` are x's
+    ``(ntw, waves, ksplit)`` or ``None`` for ``gemm_config``. ``psq_in`` are x's
     ``sumsq16`` partials (computed here when omitted); ``psq_out`` receives the
-    partials of a residual output.
+    partials of a residual output. ``workspace``: a zeroed buffer of at least
+    ``linear_workspace_bytes`` (allocated here when omitted and needed).
     """
-    _gpu(x, norm_w, residual, out, psq_in, psq_out)
+    _gpu(x, norm_w, residual, out, psq_in, psq_out, workspace)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
     M, K = x.shape
     assert K == w.K and 1 <= M <= 32, f"x [{M}, {K}] vs weight K={w.K}; M must be in [1, 32]"
@@ -279,42 +344,67 @@ def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps:
     if out is None:
         out = torch.empty((M, ncols), dtype=BF16, device=x.device)
     assert out.shape == (M, ncols) and out.is_contiguous()
-    ntw, ks = cfg if cfg is not None else gemm_config(M, w.N, K, silu_pair)
+    ntw, waves, ks = cfg if cfg is not None else gemm_config(M, w.N, K, silu_pair)
+    need = linear_workspace_bytes(M, w.N, ntw, ks)
+    if need and workspace is None:
+        workspace = linear_workspace(need, x.device)
     epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
     _lib.call("qwen_linear", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols, _nullable(norm_w),
-              _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi, ntw, ks, _stream())
+              _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi, ntw, waves, ks,
+              _nullable(workspace), 0 if workspace is None else workspace.numel(), _stream())
     return out
 
 
 def lm_head_config(M: int, N: int, K: int) -> tuple[int, int]:
-    """(ntw, ksplit) for the LM head: the vocabulary gives thousands of workgroups already."""
-    return (2, 4) if M <= 16 else (2, 2)
+    """(ntw, waves) for the LM head (measured on MI355X): the vocabulary gives thousands of
+    workgroups already; four n-tiles per workgroup share each activation load."""
+    return (2, 8) if M == 1 else (4, 8)
 
 
-def argmax_workspace_bytes(M, N, ntw) -> int:
-    return _lib.query("qwen_argmax_workspace_bytes", M, N, ntw)
+def argmax_keys(M: int, device) -> torch.Tensor:
+    """Packed (logit, index) argmax keys, zeroed; every consumer re-arms them to zero."""
+    return torch.zeros((M,), dtype=torch.int64, device=device)
 
 
 def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWeight, *, cfg=None,
-                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                   psq_in: torch.Tensor | None = None) -> torch.Tensor:
-    """Final RMSNorm + tied LM head + first-index argmax over bf16 logits -> int64 ``[M]``."""
-    _gpu(x, norm_w, out, workspace, psq_in)
+                   out: torch.Tensor | None = None, keys: torch.Tensor | None = None,
+                   psq_in: torch.Tensor | None = None, extract: bool = True) -> torch.Tensor:
+    """Final RMSNorm + tied LM head + first-index argmax over bf16 logits -> int64 ``[M]``.
+
+    ``keys``: zeroed int64 ``[M]`` packed-argmax buffer (allocated when omitted).
+    With ``extract=False`` the tokens stay in ``keys`` for ``decode_finish``.
+    """
+    _gpu(x, norm_w, out, keys, psq_in)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
     M, K = x.shape
     assert K == w.K and 1 <= M <= 32 and not w.pair
     if psq_in is None:
         psq_in = sumsq16(x)
-    ntw, ks = cfg if cfg is not None else lm_head_config(M, w.N, K)
-    need = argmax_workspace_bytes(M, w.N, ntw)
-    if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-    if out is None:
+    ntw, waves = cfg if cfg is not None else lm_head_config(M, w.N, K)
+    if keys is None:
+        keys = argmax_keys(M, x.device)
+    assert keys.dtype == torch.int64 and keys.numel() >= M and keys.is_contiguous()
+    if extract and out is None:
         out = torch.empty((M,), dtype=torch.int64, device=x.device)
     _lib.call("qwen_lm_head_argmax", x.data_ptr(), norm_w.data_ptr(), psq_in.data_ptr(), float(eps),
-              w.data.data_ptr(), M, w.N, K, workspace.data_ptr(), workspace.numel(), out.data_ptr(), ntw, ks,
+              w.data.data_ptr(), M, w.N, K, keys.data_ptr(), out.data_ptr() if extract else None, ntw, waves,
               _stream())
+    return out if extract else keys
+
+
+def argmax_extract(keys: torch.Tensor, M: int, out: torch.Tensor) -> torch.Tensor:
+    """Tokens of packed argmax keys (re-arms the keys to zero)."""
+    _lib.call("qwen_argmax_extract", keys.data_ptr(), int(M), out.data_ptr(), _stream())
     return out
+
+
+def decode_finish(keys, nxt, hist, pos, s_buf, ntarget, w: TiledWeight, h, psq) -> None:
+    """Step tail (``engine/engine.py:941-953``) + next step's embedding: token from the
+    argmax keys, history / position update, ``h = W[hist[pos]]`` and its statistics."""
+    B, cap = hist.shape
+    _lib.call("qwen_decode_finish", keys.data_ptr(), nxt.data_ptr(), hist.data_ptr(), pos.data_ptr(),
+              s_buf.data_ptr(), ntarget.data_ptr(), w.data.data_ptr(), h.data_ptr(), psq.data_ptr(), B, cap, w.N,
+              w.K, _stream())
 
 
 def embed(tok: torch.Tensor, w: TiledWeight, out: torch.Tensor | None = None,
