@@ -77,7 +77,7 @@ def parse():
 
 def profile_sample(eng, torch):
     """Dominant-kernel launches plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
-    avg_s, k_bytes = time_dominant_kernel(eng, torch, reps_per_layer=1)
+    avg_s, k_bytes, _ = time_dominant_kernel(eng, torch, reps_per_layer=1)
     n = 1 << 29                                # 2^29 bf16 = 1 GiB read + 1 GiB written per copy
     src = torch.ones(n, dtype=torch.bfloat16, device=eng.device)
     dst = torch.empty_like(src)
@@ -94,14 +94,18 @@ def profile_sample(eng, torch):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
 
 
-def measured_traffic(config: str):
+def measured_traffic(config: str, kernel: str):
+    """Bytes per launch of ``kernel`` at ``config`` from the committed PMC summary (None if absent
+    or measured for another kernel)."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
     entry = rec.get(config)
-    return None if entry is None else entry.get("bytes_per_launch")
+    if entry is None or entry.get("kernel") != kernel:
+        return None
+    return entry.get("bytes_per_launch")
 
 
 def time_dominant_kernel(eng, torch, reps_per_layer=3):
@@ -118,8 +122,11 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3):
     ops.sumsq16(h, out=psq)
 
     def run(w):
-        ops.fused_linear(h, w.w_gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq,
-                         workspace=ws)
+        if b["gemv"]:    # M <= 2: the balanced row-major GEMV the engine runs
+            ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, cfg=b["gemv_cfg"]["gu"])
+        else:
+            ops.fused_linear(h, w.w_gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq,
+                             workspace=ws)
 
     for w in eng.layers[:2]:
         run(w)
@@ -136,7 +143,9 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3):
     avg_s = start.elapsed_time(end) / 1e3 / n
     w0 = eng.layers[0].w_gu
     bytes_launch = w0.nbytes + B * w0.K * 2 + w0.K * 2 + B * (w0.N // 2) * 2
-    return avg_s, bytes_launch
+    name = ("gemv_kernel<%d, %d, true, 2>" % (B, b["gemv_cfg"]["gu"][1]) if b["gemv"]
+            else "skinny_gemm_kernel<%d, %d, %d, true, 2>" % ((2 if B > 16 else 1), cfg[0], cfg[1]))
+    return avg_s, bytes_launch, name
 
 
 def cpu_baseline(eng, cfg, B, S, layers):
@@ -241,7 +250,7 @@ def main():
 
     ctx_mid = S + 1 + W + steps / 2
     step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
-    avg_s, k_bytes = time_dominant_kernel(eng, torch)
+    avg_s, k_bytes, k_name = time_dominant_kernel(eng, torch)
     achieved = k_bytes / avg_s
     out = {
         "metric": "decode tok/s at B=1 (Qwen3-4B bf16)" if B == 1 else f"decode tok/s at B={B} (Qwen3-4B bf16)",
@@ -252,9 +261,9 @@ def main():
                 "uniform-random prompt ids (torch seed 1)",
         "config": {"workload": f"{args.config}: Qwen3-4B, B={B}, prompt {S}, {N} greedy decode steps",
                    "global_batch": B, "seq_len": S, "decode_steps": N, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "skinny_gemm norm+gate/up+SwiGLU (one layer)",
+        "roofline": {"bound": "hbm", "kernel": f"{k_name}: RMSNorm + gate/up + SwiGLU (one layer)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic(args.config),
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic(args.config, k_name),
                      "avg_us": round(avg_s * 1e6, 2), "bytes_per_launch": k_bytes},
         "step_roofline": {"bytes_per_step": int(step_bytes), "achieved_GBps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
                           "frac": round(step_bytes / (ms_step / 1e3) / HBM_PEAK, 4)},

@@ -100,6 +100,22 @@ int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int
                 const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int waves,
                 int ks, void* workspace, long long workspace_bytes, hipStream_t stream);
 
+/* Dynamic LDS bytes of a qwen_gemv launch shape (0 = unsupported shape). */
+long long qwen_gemv_lds_bytes(int M, int N, int K, int grid, int waves, int epi);
+
+/* Balanced GEMV for M <= 2 rows over a ROW-MAJOR weight (HF nn.Linear layout [N, K]):
+ * out = x @ W^T with optional RMSNorm prologue (norm_w != NULL; the row statistics are
+ * computed in the kernel from x itself) and epilogue epi = 0 store, 1 residual add
+ * (out = bf16(residual + bf16(acc)), residual may alias out), 2 SwiGLU (W = cat(gate, up)
+ * rows [2N, K]; out = bf16(bf16(silu(bf16(g))) * bf16(u)), N columns), 3 argmax of the bf16
+ * logits folded into amax[m] (same packed key as qwen_lm_head_argmax; out unused).
+ * Workgroup g of `grid` owns output rows [N*g/grid, N*(g+1)/grid), so every CU streams the
+ * same bytes; K must be a multiple of 512; waves 8 or 16. Same operator contract as
+ * qwen_linear / qwen_lm_head_argmax: replaces the projections of engine/engine.py:1108-1121
+ * (_mm / F.linear, fused_linear of engine/kernels/gemm_fused.py:136-173, lm_head + argmax). */
+int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w, float eps,
+              const void* residual, int epi, unsigned long long* amax, int grid, int waves, hipStream_t stream);
+
 /* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
  * token[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.
  * The result is folded into amax[m] (uint64: monotone logit bits << 32 | ~index), which must

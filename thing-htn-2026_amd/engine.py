@@ -161,6 +161,8 @@ class Engine:
                 setattr(w, "r_" + name, row)
             self.layers.append(w)
         self.embed = TiledWeight.random(self.V, H, [0], [_tid(None, "embed")], seed, scale, dev)
+        self.embed_rows = torch.empty((self.V, H), dtype=BF16, device=dev)
+        ops.init_weight(self.embed_rows, self.V, H, False, False, [0], [_tid(None, "embed")], seed, scale)
         self.final_norm = ones_h.clone()
 
     def _load_safetensors(self, model_path):
@@ -198,9 +200,9 @@ class Engine:
             self.layers.append(w)
         emb = get("model.embed_tokens.weight")
         self.embed = ops.tile_weight(emb)
+        self.embed_rows = emb          # row-major copy: the M <= 2 LM head streams it
         if "lm_head.weight" in tensors and not self.cfg.get("tie_word_embeddings", True):
             raise RuntimeError("untied LM head is not supported (Qwen3-4B ties it to the embedding)")
-        del emb
         self.final_norm = get("model.norm.weight")
         del tensors
 
@@ -268,6 +270,14 @@ class Engine:
             }
             n_of = {"qkv": W_qkv, "o": self.H, "gu": 2 * self.I, "down": self.H}
             ws = max(ops.linear_workspace_bytes(M, n_of[k], c[0], c[2]) for k, c in cfg.items())
+            gemv = M <= ops.GEMV_MAX_M
+            gemv_cfg = {
+                "qkv": ops.gemv_config(M, W_qkv, self.H, ops.GEPI_STORE, dev),
+                "o": ops.gemv_config(M, self.H, self.Nq * self.D, ops.GEPI_RES, dev),
+                "gu": ops.gemv_config(M, self.I, self.H, ops.GEPI_SWIGLU, dev),
+                "down": ops.gemv_config(M, self.H, self.I, ops.GEPI_RES, dev),
+                "lm": ops.gemv_config(M, self.V, self.H, ops.GEPI_ARGMAX, dev),
+            } if gemv else None
             self.bufs[key] = {
                 "h": torch.zeros((M, self.H), dtype=BF16, device=dev),
                 "qkv": torch.empty((M, W_qkv), dtype=BF16, device=dev),
@@ -281,6 +291,8 @@ class Engine:
                 "attn_ws": ops.attn_workspace(B, T, self.Nq, self.Nkv, self.D, S, dev),
                 "gemm_ws": ops.linear_workspace(ws, dev),
                 "cfg": cfg,
+                "gemv": gemv,
+                "gemv_cfg": gemv_cfg,
                 "lm_cfg": ops.lm_head_config(M, self.V, self.H),
             }
         return self.bufs[key]
@@ -308,20 +320,37 @@ class Engine:
             ops.embed(tok.reshape(-1), self.embed, out=h, psq_out=psq)
         else:
             assert T == 1
+        gc = b["gemv_cfg"]
         for l, w in enumerate(self.layers):
-            ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq, workspace=ws)
+            # M <= 2: balanced row-major GEMVs (RMSNorm statistics computed in-kernel);
+            # larger M: MFMA kernels over the tiled weights, statistics from psq.
+            if gc is not None:
+                ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
+            else:
+                ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq,
+                                 workspace=ws)
             ops.attn_decode_fused(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
                                   self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
                                   workspace=b["attn_ws"], waves=b["attn_waves"])
-            ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
-            ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, psq_in=psq,
-                             workspace=ws)
-            ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
+            if gc is not None:
+                ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
+                ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, cfg=gc["gu"])
+                ops.gemv(p, w.r_down, residual=h, out=h, cfg=gc["down"])
+            else:
+                ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
+                ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p,
+                                 psq_in=psq, workspace=ws)
+                ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
             if hidden is not None:
                 hidden.append(h.clone())
         extract = tok is not None
-        ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"], out=b["next"] if extract else None,
-                           keys=b["keys"], psq_in=psq, extract=extract)
+        if gc is not None:
+            ops.gemv(h, self.embed_rows, norm_w=self.final_norm, eps=self.eps, amax=b["keys"], cfg=gc["lm"])
+            if extract:
+                ops.argmax_extract(b["keys"], M, b["next"])
+        else:
+            ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"],
+                               out=b["next"] if extract else None, keys=b["keys"], psq_in=psq, extract=extract)
         return b["next"]
 
     def _plain_step(self):

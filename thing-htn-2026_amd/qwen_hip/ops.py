@@ -113,6 +113,8 @@ def choose_num_splits(B: int, Nkv: int, cap: int, T: int = 1) -> int:
     slots per split; power of two in [1, 64]. Fixed per captured graph, as in
     the reference (``attention.py:94-110``), where the target was 264 programs.
     """
+    if B * Nkv * T <= 8:   # one sequence: the cross-workgroup merge costs more than it saves (measured)
+        return 1
     want = max(1, math.ceil(256 / max(1, B * Nkv * T)))
     limit = max(1, cap // 128)
     s = 1
@@ -122,9 +124,10 @@ def choose_num_splits(B: int, Nkv: int, cap: int, T: int = 1) -> int:
 
 
 def attn_waves(B: int, T: int) -> int:
-    """Wavefronts per attention workgroup (measured): 4 for latency-bound small batches,
-    8 once the context stream dominates."""
-    return 8 if B * T >= 8 and T == 1 else 4
+    """Wavefronts per attention workgroup (measured on MI355X at B = 1, 8, 32): 4 up to eight
+    query rows, 8 once the context stream dominates."""
+    return 8 if B * T >= 16 and T == 1 else 4
+
 
 
 ATTN_WAVES = 8   # wavefronts per attention workgroup
@@ -353,6 +356,62 @@ def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps:
               _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi, ntw, waves, ks,
               _nullable(workspace), 0 if workspace is None else workspace.numel(), _stream())
     return out
+
+
+GEMV_MAX_M = 2   # rows handled by the balanced row-major GEMV (qwen_gemv)
+GEPI_STORE, GEPI_RES, GEPI_SWIGLU, GEPI_ARGMAX = 0, 1, 2, 3
+
+
+def cu_count(device=None) -> int:
+    return torch.cuda.get_device_properties(device if device is not None else 0).multi_processor_count
+
+
+def gemv_config(M: int, N: int, K: int, epi: int, device=None) -> tuple[int, int]:
+    """(grid, waves) for qwen_gemv (measured on MI355X, graph-replayed over 36 layers): one
+    workgroup of 8 wavefronts per CU, so every CU streams the same bytes; the SwiGLU projection
+    (the largest) runs two workgroups per CU."""
+    cus = cu_count(device)
+    return (2 * cus if epi == GEPI_SWIGLU else cus), 8
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, residual=None, silu_pair: bool = False,
+         out: torch.Tensor | None = None, amax: torch.Tensor | None = None, cfg=None) -> torch.Tensor:
+    """``x @ w.T`` for ``x [M <= 2, K]`` over a row-major ``w [N, K]`` (``gemm_fused.py:136-173``
+    semantics): optional RMSNorm prologue (``norm_w``), residual or SwiGLU epilogue
+    (``silu_pair``: ``w = cat(gate, up)`` rows, output ``[M, N/2]``), or, with ``amax``, the
+    first-index argmax of the bf16 logits folded into the packed int64 keys (LM head).
+    """
+    _gpu(x, w, norm_w, residual, out, amax)
+    assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
+    assert w.dtype == BF16 and w.dim() == 2 and w.is_contiguous()
+    M, K = x.shape
+    assert 1 <= M <= GEMV_MAX_M and w.shape[1] == K and K % 512 == 0, f"gemv: x [{M}, {K}], w {tuple(w.shape)}"
+    if amax is not None:
+        epi = GEPI_ARGMAX
+        assert norm_w is not None and residual is None and not silu_pair
+        assert amax.dtype == torch.int64 and amax.numel() >= M and amax.is_contiguous()
+    elif silu_pair:
+        epi = GEPI_SWIGLU
+        assert norm_w is not None and residual is None and w.shape[0] % 2 == 0
+    elif residual is not None:
+        epi = GEPI_RES
+        assert norm_w is None
+    else:
+        epi = GEPI_STORE
+    N = w.shape[0] // 2 if silu_pair else w.shape[0]
+    if norm_w is not None:
+        assert norm_w.dtype == BF16 and norm_w.numel() == K and norm_w.is_contiguous()
+    if epi != GEPI_ARGMAX:
+        if residual is not None:
+            assert residual.shape == (M, N) and residual.dtype == BF16 and residual.is_contiguous()
+        if out is None:
+            out = torch.empty((M, N), dtype=BF16, device=x.device)
+        assert out.shape == (M, N) and out.is_contiguous() and out.dtype == BF16
+    grid, waves = cfg if cfg is not None else gemv_config(M, N, K, epi, x.device)
+    _lib.call("qwen_gemv", x.data_ptr(), w.data_ptr(), _nullable(out) if epi != GEPI_ARGMAX else None, M, N, K,
+              N, _nullable(norm_w), float(eps), _nullable(residual), epi, _nullable(amax), int(grid), int(waves),
+              _stream())
+    return amax if epi == GEPI_ARGMAX else out
 
 
 def lm_head_config(M: int, N: int, K: int) -> tuple[int, int]:
