@@ -61,6 +61,11 @@ def kv_bytes_per_token(cfg) -> int:
     return cfg["num_hidden_layers"] * 2 * cfg["num_key_value_heads"] * cfg["head_dim"] * 2
 
 
+def eng_pipeline_depth() -> int:
+    from engine import CONFIG
+    return CONFIG["pipeline_depth"]
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -244,6 +249,9 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     steps = eng.decode_launches - l0
+    if steps <= 0:
+        sys.exit(f"bench.py: no decode step was launched inside the timed window (--steps {K} is within the "
+                 f"engine's {eng_pipeline_depth()} steps of pipelining); use more steps")
     dt = t1 - t0
     tok_s = steps * B / dt
     ms_step = dt / steps * 1e3

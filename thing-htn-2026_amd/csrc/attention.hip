@@ -40,6 +40,7 @@ constexpr int ATT_D = 128;
 constexpr int G = 4;                       // query heads per KV head
 constexpr int KU = 2;                      // keys per slot per iteration
 constexpr int KPI = 8 * KU;                // keys per wavefront iteration
+constexpr int MERGE_BATCH = 8;             // split partials fetched in one round trip by the last arriver
 
 struct AttnParams {
   const bf16_t* q;          // [B, T, Nq, D] (unfused)
@@ -260,6 +261,17 @@ __global__ void __launch_bounds__(64 * WPG) attn_kernel(AttnParams p) {
         s[u][g] = valid[u] ? d * p.scale : NEG_BIG;
       }
     }
+    // PV operands: the two keys of a slot paired per dimension, (V0[d], V1[d]) as a bf16x2,
+    // so each head's update is one v_dot2_f32_bf16 per dimension (shared by the four heads).
+    static_assert(KU == 2, "key pairing assumes two keys per slot");
+    uint32_t vp[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w0 = i < 4 ? (&r.v[0][0].x)[i] : (&r.v[0][1].x)[i - 4];
+      const uint32_t w1 = i < 4 ? (&r.v[1][0].x)[i] : (&r.v[1][1].x)[i - 4];
+      vp[2 * i] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);      // (V0[2i],   V1[2i])
+      vp[2 * i + 1] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);  // (V0[2i+1], V1[2i+1])
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mn = m[g];
@@ -274,18 +286,17 @@ __global__ void __launch_bounds__(64 * WPG) attn_kernel(AttnParams p) {
         pb[u] = rbf(pr);  // P rounded to bf16 for the PV product
       }
       l[g] = l[g] * alpha + psum;
+      // alpha is exactly 1 where no slot's running max moved: skip the (exact) no-op rescale
+      // when that holds for the whole wavefront.
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[g][e] *= alpha;
-#pragma unroll
-      for (int u = 0; u < KU; ++u) {
-        const uint32_t vw[8] = {r.v[u][0].x, r.v[u][0].y, r.v[u][0].z, r.v[u][0].w,
-                                r.v[u][1].x, r.v[u][1].y, r.v[u][1].z, r.v[u][1].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          acc[g][2 * i] = fmaf(pb[u], __uint_as_float(vw[i] << 16), acc[g][2 * i]);
-          acc[g][2 * i + 1] = fmaf(pb[u], __uint_as_float(vw[i] & 0xffff0000u), acc[g][2 * i + 1]);
-        }
+        for (int e = 0; e < 16; ++e) acc[g][e] *= alpha;
       }
+      const bf16x2_t pp = __builtin_bit_cast(
+          bf16x2_t, (__float_as_uint(pb[0]) >> 16) | (__float_as_uint(pb[1]) & 0xffff0000u));  // exact: bf16 values
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[g][e] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2_t, vp[e]), acc[g][e], false);
       m[g] = mn;
     }
   };
@@ -381,16 +392,44 @@ __global__ void __launch_bounds__(64 * WPG) attn_kernel(AttnParams p) {
   if (old != (unsigned)(p.S - 1)) return;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const float* all = p.part + (row * p.S * G + g) * PW;
-  float MM = NEG_BIG;
-  for (int s = 0; s < p.S; ++s) MM = fmaxf(MM, s == split ? M : load_dev(all + (long long)s * G * PW));
   float LL = 0.f, oo[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < p.S; ++s) {
-    const float* ps = all + (long long)s * G * PW;
-    const bool own = s == split;
-    const float sc = __expf((own ? M : load_dev(ps)) - MM);
-    LL += sc * (own ? L : load_dev(ps + 1));
+  if (p.S <= MERGE_BATCH) {
+    // Every split's partial requested at once (one round trip), merged in split order.
+    float ms[MERGE_BATCH], ls[MERGE_BATCH], os[MERGE_BATCH][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) oo[e] += sc * (own ? o[e] : load_dev(ps + 2 + d0 + e));
+    for (int s = 0; s < MERGE_BATCH; ++s) {
+      const int sl = s < p.S ? s : split;  // slots past S repeat this split's own (ignored below)
+      const float* ps = all + (long long)sl * G * PW;
+      ms[s] = load_dev(ps);
+      ls[s] = load_dev(ps + 1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) os[s][e] = load_dev(ps + 2 + d0 + e);
+    }
+    float MM = NEG_BIG;
+#pragma unroll
+    for (int s = 0; s < MERGE_BATCH; ++s)
+      if (s < p.S) MM = fmaxf(MM, s == split ? M : ms[s]);
+#pragma unroll
+    for (int s = 0; s < MERGE_BATCH; ++s) {
+      if (s < p.S) {
+        const bool own = s == split;
+        const float sc = __expf((own ? M : ms[s]) - MM);
+        LL += sc * (own ? L : ls[s]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) oo[e] += sc * (own ? o[e] : os[s][e]);
+      }
+    }
+  } else {
+    float MM = NEG_BIG;
+    for (int s = 0; s < p.S; ++s) MM = fmaxf(MM, s == split ? M : load_dev(all + (long long)s * G * PW));
+    for (int s = 0; s < p.S; ++s) {
+      const float* ps = all + (long long)s * G * PW;
+      const bool own = s == split;
+      const float sc = __expf((own ? M : load_dev(ps)) - MM);
+      LL += sc * (own ? L : load_dev(ps + 1));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) oo[e] += sc * (own ? o[e] : load_dev(ps + 2 + d0 + e));
+    }
   }
   float r[8];
 #pragma unroll
