@@ -2,6 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
 
+c5 (speculative verify steps) reports verify steps/s instead of decoded tokens/s.
+
 Default workload is BASELINE.json's configs[1] ("c2"): Qwen3-4B, random-init
 bf16 weights (seed 0), batch 1, a 128-token uniform-random prompt, greedy
 decoding. The engine's own generate() runs the prompt forward (untimed) and
@@ -39,7 +41,9 @@ CONFIGS = {
     "c2": (1, 128, 256),
     "c3": (8, 2048, 512),
     "c4": (32, 8192, 256),
+    "c5": (4, 4096, 200),     # speculative verify steps, T = SPEC_T tokens per sequence
 }
+SPEC_T = 5                    # c5: 1 accepted + 4 draft tokens per verify step
 QWEN3_4B = {
     "hidden_size": 2560, "intermediate_size": 9728, "vocab_size": 151936,
     "num_hidden_layers": 36, "num_attention_heads": 32, "num_key_value_heads": 8,
@@ -80,9 +84,9 @@ def parse():
     return p.parse_args()
 
 
-def profile_sample(eng, torch):
+def profile_sample(eng, torch, T=1):
     """Dominant-kernel launches plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
-    avg_s, k_bytes, _ = time_dominant_kernel(eng, torch, reps_per_layer=1)
+    avg_s, k_bytes, _ = time_dominant_kernel(eng, torch, reps_per_layer=1, T=T)
     n = 1 << 29                                # 2^29 bf16 = 1 GiB read + 1 GiB written per copy
     src = torch.ones(n, dtype=torch.bfloat16, device=eng.device)
     dst = torch.empty_like(src)
@@ -113,15 +117,15 @@ def measured_traffic(config: str, kernel: str):
     return entry.get("bytes_per_launch")
 
 
-def time_dominant_kernel(eng, torch, reps_per_layer=3):
-    """Average duration of the fused norm + gate/up + SwiGLU GEMM at the bench's M.
+def time_dominant_kernel(eng, torch, reps_per_layer=3, T=1):
+    """Average duration of the fused norm + gate/up + SwiGLU GEMM at the bench's M = B * T.
 
     Timed with HIP events on the stream the kernel is launched on, rotating over
     the 36 layers' weights (3.6 GB) so that nothing is served from cache.
     """
     from qwen_hip import ops
     B = eng.B
-    b = eng._buffers(B, 1)
+    b = eng._buffers(B, T)
     h, p, psq, cfg, ws = b["h"], b["p"], b["psq"], b["cfg"]["gu"], b["gemm_ws"]
     stream = torch.cuda.current_stream()
     ops.sumsq16(h, out=psq)
@@ -147,10 +151,55 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3):
     end.synchronize()
     avg_s = start.elapsed_time(end) / 1e3 / n
     w0 = eng.layers[0].w_gu
-    bytes_launch = w0.nbytes + B * w0.K * 2 + w0.K * 2 + B * (w0.N // 2) * 2
-    name = ("gemv_kernel<%d, %d, true, 2>" % (B, b["gemv_cfg"]["gu"][1]) if b["gemv"]
-            else "skinny_gemm_kernel<%d, %d, %d, true, 2>" % ((2 if B > 16 else 1), cfg[0], cfg[1]))
+    M = B * T
+    bytes_launch = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
+    name = ("gemv_kernel<%d, %d, true, 2>" % (M, b["gemv_cfg"]["gu"][1]) if b["gemv"]
+            else "skinny_gemm_kernel<%d, %d, %d, true, 2>" % ((2 if M > 16 else 1), cfg[0], cfg[1]))
     return avg_s, bytes_launch, name
+
+
+def bench_verify(eng, torch, cfg, B, S, K, W):
+    """c5: K speculative verify steps (T = SPEC_T tokens per sequence: the last accepted token and
+    SPEC_T - 1 prompt-lookup drafts, which on a uniform-random prompt are effectively random ids),
+    each one replay of the captured verify graph (draft, 36 layers over B*T rows with causal
+    multi-query attention, argmax per position, acceptance). ``value`` = verify steps per second."""
+    T = SPEC_T
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
+    eng.start(prompt, T * (K + W) + 8)
+    assert eng.k_active == T - 1 and T in eng.graphs, "verify graph not captured"
+    graph = eng.graphs[T][0]
+    for _ in range(W):
+        graph.replay()
+    torch.cuda.synchronize()
+    pos0 = int(eng.pos_buf[0])
+    t0 = time.perf_counter()
+    for _ in range(K):
+        graph.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ctx_mid = (pos0 + int(eng.pos_buf[0])) / 2 + T
+    step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
+    avg_s, k_bytes, k_name = time_dominant_kernel(eng, torch, T=T)
+    achieved = k_bytes / avg_s
+    return {
+        "metric": f"spec-verify steps/s at B={B}, T={T}, context {S} (Qwen3-4B bf16)",
+        "value": round(K / dt, 2), "unit": "verify steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(dt / K * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (counter-based generator, seed 0, std 0.02), uniform-random "
+                "prompt ids (torch seed 1); drafts by prompt lookup (no repeats: effectively random ids)",
+        "config": {"workload": f"c5: Qwen3-4B, B={B}, context {S}, T={T} verify steps",
+                   "global_batch": B, "seq_len": S, "verify_tokens": T, "parallelism": "single GPU"},
+        "positions_per_s": round(K * B * T / dt, 1),
+        "roofline": {"bound": "hbm", "kernel": f"{k_name}: RMSNorm + gate/up + SwiGLU (one layer)",
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic("c5", k_name),
+                     "avg_us": round(avg_s * 1e6, 2), "bytes_per_launch": k_bytes},
+        "step_roofline": {"bytes_per_step": int(step_bytes),
+                          "achieved_GBps": round(step_bytes * K / dt / 1e9, 1),
+                          "frac": round(step_bytes * K / dt / HBM_PEAK, 4)},
+    }
 
 
 def cpu_baseline(eng, cfg, B, S, layers):
@@ -226,11 +275,17 @@ def main():
     K = args.steps if args.steps is not None else N
     W = args.warmup
     cfg = QWEN3_4B
+    if args.config == "c5":
+        import engine as engine_mod
+        engine_mod.CONFIG["spec_k"] = SPEC_T - 1
     with tempfile.TemporaryDirectory() as d:
         eng = Engine(write_random_model(d, cfg, seed=0, std=0.02))
+    if args.config == "c5" and not args.profile_sample:
+        print(json.dumps(bench_verify(eng, torch, cfg, B, S, K, W)), flush=True)
+        return
     if args.profile_sample:
         eng._prepare(B, S, K + W + 1)
-        print(json.dumps(profile_sample(eng, torch)), flush=True)
+        print(json.dumps(profile_sample(eng, torch, T=SPEC_T if args.config == "c5" else 1)), flush=True)
         return
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()

@@ -146,6 +146,23 @@ int qwen_decode_finish(unsigned long long* amax, int64_t* next, int64_t* hist, i
                        const int64_t* ntarget, const void* w_tiled, void* h, float* psq, int B, int cap, long long V,
                        int K, hipStream_t stream);
 
+/* Prompt-lookup draft for a speculative verify step: for each sequence b with L = pos[b] + 1
+ * valid history tokens, the latest start i < L - n with hist[b, i..i+n-1] == hist[b, L-n..L-1]
+ * (i = -1 if none) gives tok_out[b] = [hist[b, L-1], hist[b, clamp(i+n+j, 0, L-1)] for j < k]
+ * ([B, k+1] int64). 1 <= k <= 15, 1 <= n <= 8. Replaces engine/engine.py:955-977 (_spec_draft). */
+int qwen_spec_draft(const int64_t* hist, const int32_t* pos, int B, int cap, int k, int n, int64_t* tok_out,
+                    hipStream_t stream);
+
+/* Acceptance of a verify step of T = k+1 tokens: nxt [B*T] (greedy token after each fed prefix),
+ * tok [B, T] (fed ids). adv[b] = 1 + (leading drafts equal to the model's tokens), 0 for rows that
+ * already produced their tokens ((pos+1 - s_buf) >= ntarget); hist[b, pos[b]+1+j] = nxt[b, j] for
+ * j < adv (other positions to the dump slot cap-1); pos[b] += adv; out_t [T, B] = nxt transposed;
+ * then h[b] = W[hist[b, pos[b]]] from the tiled table and psq its qwen_sumsq16 partials (a plain
+ * step may follow). Replaces engine/engine.py:994-1003 (the tail of _spec_step). */
+int qwen_spec_accept(const int64_t* nxt, const int64_t* tok, int64_t* hist, int32_t* pos, const int64_t* s_buf,
+                     const int64_t* ntarget, int B, int cap, int T, int64_t* out_t, int64_t* adv_out,
+                     const void* w_tiled, void* h, float* psq, long long V, int K, hipStream_t stream);
+
 /* Row-major [N, K] bf16 -> tiled layout (pair = 1: gate|up interleave, tile 2p = rows
  * 16p.., tile 2p+1 = rows N/2 + 16p..). Replaces the weight fusion / layout step of
  * engine/engine.py:209-227 (the reference keeps row-major; this build re-lays for MFMA). */

@@ -75,6 +75,34 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Row `id` (clamped into [0, V)) of a tiled [V, K] table -> hrow [K] bf16 and its
+// per-16-column sums of squares psq_row [K/16] (the next RMSNorm's statistics).
+// Called by a whole workgroup of `nthreads` threads (a multiple of 64).
+// Tiled layout: element (n, k) sits in tile (n/16, k/32) at lane 16*((k%32)/8) + n%16.
+__device__ __forceinline__ void embed_row_tiled(const bf16_t* __restrict__ w, long long id, long long V, int K,
+                                                bf16_t* __restrict__ hrow, float* __restrict__ psq_row, int tid,
+                                                int nthreads) {
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+  const long long KT = K / 32;
+  const long long nt = id >> 4;
+  const int r = (int)(id & 15);
+  const int kc = K / 8;
+  for (int c0 = 0; c0 < kc; c0 += nthreads) {
+    const int cl = c0 + tid;
+    const bool live = cl < kc;
+    const int chunk = live ? cl : 0;  // dead lanes redo chunk 0 so the pair shuffle stays uniform
+    const int kt = chunk >> 2, q = chunk & 3;
+    const uint4 v = reinterpret_cast<const uint4*>(w)[(nt * KT + kt) * 64 + q * 16 + r];
+    if (live) reinterpret_cast<uint4*>(hrow)[chunk] = v;
+    float f[8], s = 0.f;
+    unpack8(v, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
+    s += __shfl_xor(s, 1, 64);
+    if (live && (chunk & 1) == 0) psq_row[chunk >> 1] = s;
+  }
+}
+
 static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
 
 // Launch-status check used by every entry point: returns the launch error.

@@ -38,25 +38,7 @@ __global__ void __launch_bounds__(FIN_THREADS) decode_finish_kernel(
     amax[b] = 0ull;
   }
   // Embedding gather from the tiled table (ids clamped into [0, V)).
-  id = id < 0 ? 0 : (id >= V ? V - 1 : id);
-  const long long KT = K / 32;
-  const long long nt = id >> 4;
-  const int r = (int)(id & 15);
-  const int kc = K / 8;
-  for (int c0 = 0; c0 < kc; c0 += FIN_THREADS) {
-    const int cl = c0 + threadIdx.x;
-    const bool live = cl < kc;
-    const int chunk = live ? cl : 0;  // dead lanes redo chunk 0 so the pair shuffle stays uniform
-    const int kt = chunk >> 2, q = chunk & 3;
-    const uint4 v = reinterpret_cast<const uint4*>(w)[(nt * KT + kt) * 64 + q * 16 + r];
-    if (live) reinterpret_cast<uint4*>(h + (long long)b * K)[chunk] = v;
-    float f[8], s = 0.f;
-    unpack8(v, f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s = add_rn(s, mul_rn(f[e], f[e]));
-    s += __shfl_xor(s, 1, 64);
-    if (live && (chunk & 1) == 0) psq[(long long)b * (K / 16) + (chunk >> 1)] = s;
-  }
+  embed_row_tiled(w, id, V, K, h + (long long)b * K, psq + (long long)b * (K / 16), threadIdx.x, FIN_THREADS);
 }
 
 }  // namespace

@@ -18,6 +18,12 @@ graph (``torch.cuda.CUDAGraph``) and replayed per token:
     final norm + LM head + argmax                      1 kernel
     token / history / position update + next embedding 1 kernel
 
+With ``CONFIG["spec_k"] = k > 0`` (exact speculative decoding, off by default as in
+the reference) a second graph verifies k prompt-lookup drafts per sequence in one
+T = k + 1 step: draft kernel | the same per-layer kernels over B*T rows | accept
+kernel (history scatter, position advance, next input row); the decode loop picks
+verify or plain steps adaptively.
+
 Torch is used for device memory, the KV cache, the RoPE tables, graph
 capture, host<->device copies and (for now) the prompt forward's large GEMMs
 and causal attention (hipBLASLt / SDPA flash), whose norms, RoPE, cache writes
@@ -48,6 +54,12 @@ CONFIG = {
     "pipeline_depth": 3,     # decode steps in flight ahead of the host yield (engine/engine.py:71)
     "prefill_rows": 32768,   # max B*S rows per prompt-forward batch slice (engine/engine.py:72)
     "cap_align": 64,         # KV-cache capacity alignment (engine/engine.py:73)
+    # Exact speculative decoding (engine/engine.py:79-82): prompt-lookup drafts of spec_k tokens
+    # verified in one T = spec_k + 1 step; 0 = off (the reference's default).
+    "spec_k": int(os.environ.get("QWEN_ENGINE_SPEC_K", "0")),
+    "spec_n": 3,             # n-gram length of the draft lookup
+    "spec_max_batch": 8,     # speculate only when B <= this (and B * (spec_k + 1) <= 32)
+    "spec_probe": (24, 6),   # while speculation loses: plain steps between probes, spec steps per probe
     "log": True,
 }
 
@@ -119,6 +131,9 @@ class Engine:
         self.step_ms = {}
         self.sdpa_mode = None
         self.decode_launches = 0   # decode steps launched since load (benchmarks read it)
+        self.spec_launches = 0     # of which speculative verify steps
+        self.spec_tokens = 0       # tokens the slowest unfinished row gained from them
+        self.k_active = 0          # draft tokens per verify step for the prepared batch (0: plain only)
         self._load_weights(model_path)
         self._rope_max = 0
         self._ensure_rope(8192)
@@ -229,11 +244,14 @@ class Engine:
         """Per-shape state (``engine/engine.py:830-863``): KV cache, history, buffers, graph."""
         if B > 32:
             raise ValueError("this engine decodes at most 32 sequences per call")
-        slack = (CONFIG["pipeline_depth"] + 3) + 16
+        k = int(CONFIG["spec_k"])
+        if not (0 < k <= 15 and B <= CONFIG["spec_max_batch"] and B * (k + 1) <= 32):
+            k = 0
+        slack = (CONFIG["pipeline_depth"] + 3) * (k + 1) + 16
         align = CONFIG["cap_align"]
         cap = ((S + N + slack + align - 1) // align) * align
         self._ensure_rope(cap)
-        if B != self.B or cap > self.CAP:
+        if B != self.B or cap > self.CAP or k != getattr(self, "k_active", 0):
             torch.cuda.synchronize()
             self.graphs = {}
             self.k_cache = self.v_cache = None
@@ -246,14 +264,18 @@ class Engine:
             self.pos_buf = torch.zeros((B,), dtype=torch.int32, device=dev)
             self.s_buf = torch.zeros((1,), dtype=torch.int64, device=dev)
             self.ntarget_buf = torch.full((1,), 1 << 40, dtype=torch.int64, device=dev)
-            self.B, self.CAP = B, cap
+            self.B, self.CAP, self.k_active = B, cap, k
             self.bufs = {}
             ring = CONFIG["pipeline_depth"] + 2
-            self.pin_nxt = [torch.zeros((B,), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
+            self.pin_nxt = [torch.zeros((k + 1, B), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
+            self.pin_adv = [torch.zeros((B,), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
             self.events = [torch.cuda.Event() for _ in range(ring)]
-            _log(f"state B={B} CAP={cap} kv={2 * self.L * B * self.Nkv * cap * self.D * 2 / 2**30:.2f}GiB")
-        if CONFIG["graphs"] and 1 not in self.graphs:
-            self._capture(1)
+            _log(f"state B={B} CAP={cap} spec_k={k} "
+                 f"kv={2 * self.L * B * self.Nkv * cap * self.D * 2 / 2**30:.2f}GiB")
+        if CONFIG["graphs"]:
+            for T in (1, k + 1) if k else (1,):
+                if T not in self.graphs:
+                    self._capture(T)
 
     def _buffers(self, B, T):
         """Static activation buffers for a (B, T) step, reused by every replay."""
@@ -285,6 +307,9 @@ class Engine:
                 "p": torch.empty((M, self.I), dtype=BF16, device=dev),
                 "psq": torch.zeros((M, self.H // 16), dtype=torch.float32, device=dev),
                 "next": torch.empty((M,), dtype=torch.int64, device=dev),
+                "tok": torch.zeros((B, T), dtype=torch.int64, device=dev),      # verify-step input ids
+                "out_t": torch.zeros((T, B), dtype=torch.int64, device=dev),    # verify-step tokens, [T, B]
+                "adv": torch.zeros((B,), dtype=torch.int64, device=dev),        # accepted tokens per row
                 "keys": ops.argmax_keys(M, dev),
                 "splits": S,
                 "attn_waves": ops.attn_waves(B, T),
@@ -367,6 +392,19 @@ class Engine:
         b = self._buffers(self.B, 1)
         ops.embed_hist(self.hist_buf, self.pos_buf, self.embed, b["h"], psq_out=b["psq"])
 
+    def _spec_step(self, k):
+        """``_spec_step`` (``engine/engine.py:979-1003``): draft ``k`` tokens per sequence by prompt
+        lookup, verify them in one T = k+1 step, accept the leading matches. Returns ``(out_t [T, B],
+        adv [B])``; also leaves the embedding of the new ``hist[pos]`` in the plain step's input rows."""
+        B, T = self.B, k + 1
+        b = self._buffers(B, T)
+        b1 = self._buffers(B, 1)
+        ops.spec_draft(self.hist_buf, self.pos_buf, k, CONFIG["spec_n"], out=b["tok"])
+        nxt = self._step(T, tok=b["tok"])
+        ops.spec_accept(nxt, b["tok"], self.hist_buf, self.pos_buf, self.s_buf, self.ntarget_buf, self.embed,
+                        b1["h"], b1["psq"], b["out_t"], b["adv"])
+        return b["out_t"], b["adv"]
+
     def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
         """Greedy next token at every position of ``tok [B, T]`` (the speculative verify forward
         of ``engine/engine.py:979-993``): token ``t`` of row ``b`` sits at ``positions[b] + t``;
@@ -389,35 +427,43 @@ class Engine:
         return [h.clone() for h in hidden]
 
     def _capture(self, T):
-        """Record one plain decode step into a HIP graph (``engine/engine.py:1005-1042``)."""
-        assert T == 1
+        """Record one decode step into a HIP graph (``engine/engine.py:1005-1042``): the plain step
+        (T = 1) or the speculative verify step (T = k + 1)."""
+        k = T - 1
+        run = self._plain_step if k == 0 else (lambda: self._spec_step(k))
         pos_saved = self.pos_buf.clone()
         hist_saved = self.hist_buf.clone()
+        s_saved, n_saved = self.s_buf.clone(), self.ntarget_buf.clone()
+        self.s_buf.zero_()
+        self.ntarget_buf.fill_(1 << 40)
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
             self.pos_buf.fill_(1)
-            self._plain_step()              # warm-up (allocates nothing new)
+            run()                           # warm-up (allocates nothing new)
         torch.cuda.current_stream().wait_stream(stream)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         self.pos_buf.fill_(1)
         with torch.cuda.graph(graph):
-            out = self._plain_step()
+            out = run()
         torch.cuda.synchronize()
         self.graphs[T] = (graph, out)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        self.pos_buf.fill_(1)
+        reps = 5
         start.record()
-        for _ in range(5):
+        for _ in range(reps):
+            self.pos_buf.fill_(1)
             graph.replay()
         end.record()
         torch.cuda.synchronize()
-        self.step_ms[T] = start.elapsed_time(end) / 5
-        # Capture wrote K/V at slot 1 and hist[:, 2]: the prompt forward and the
+        self.step_ms[T] = start.elapsed_time(end) / reps
+        # Capture wrote K/V at slots 1..T and hist[:, 2..T+1]: the prompt forward and the
         # first decode steps overwrite those slots before anything reads them.
         self.pos_buf.copy_(pos_saved)
         self.hist_buf.copy_(hist_saved)
+        self.s_buf.copy_(s_saved)
+        self.ntarget_buf.copy_(n_saved)
         torch.cuda.synchronize()
         _log(f"captured T={T} graph; replay {self.step_ms[T]:.3f} ms/step")
 
@@ -514,6 +560,15 @@ class Engine:
             return
         if any(len(row) != S for row in input_ids):
             raise ValueError("all prompts must have the same length")
+        with torch.inference_mode():
+            first = self.start(input_ids, N)
+            yield from self._decode_loop(first, B, N)
+
+    def start(self, input_ids: list[list[int]], max_new_tokens: int) -> torch.Tensor:
+        """The part of ``generate`` before the first yield (``engine/engine.py:1225-1248``): per-shape
+        state, prompt forward, history and positions, the first decode step's input row. Returns the
+        first token of every sequence (``[B]`` int64 on the device)."""
+        B, S, N = len(input_ids), len(input_ids[0]), int(max_new_tokens)
         ids_cpu = torch.tensor(input_ids, dtype=torch.int64)
         if ids_cpu.numel() and (int(ids_cpu.min()) < 0 or int(ids_cpu.max()) >= self.V):
             raise ValueError(f"token ids must lie in [0, {self.V})")
@@ -527,44 +582,105 @@ class Engine:
             self.s_buf.fill_(S)
             self.ntarget_buf.fill_(N)
             self._prime()
-            yield from self._decode_loop(first, B, N)
+        return first
 
     def _decode_loop(self, first, B, N):
         """Pipelined graph replays with async D2H copies into a pinned ring (``engine/engine.py:1254-1378``).
 
-        At most ``pipeline_depth + 1`` steps are in flight, and exactly N - 1
-        decode steps are launched (never one more than needed).
+        At most ``pipeline_depth + 1`` steps are in flight, and no step is launched that could
+        not contribute a token (``:1332-1336``). With speculation on, the loop alternates between
+        verify steps and plain steps: it speculates while the accepted tokens per verify step
+        (moving average of the slowest unfinished row) times the plain step time beat the verify
+        step time, and otherwise runs plain steps, probing speculation again every so often
+        (``:1319-1372``).
         """
         depth = CONFIG["pipeline_depth"]
         ring = len(self.pin_nxt)
         stream = torch.cuda.current_stream()
-        graph_out = self.graphs.get(1)
+        k = self.k_active
+        T = k + 1
+        graphs = self.graphs
 
         def launch(slot, mode):
             if mode == "first":
-                self.pin_nxt[slot].copy_(first, non_blocking=True)
-            else:
-                if graph_out is not None:
-                    graph_out[0].replay()
-                    out = graph_out[1]
+                self.pin_nxt[slot][0].copy_(first, non_blocking=True)
+            elif mode == "plain":
+                if 1 in graphs:
+                    graphs[1][0].replay()
+                    out = graphs[1][1]
                 else:
                     out = self._plain_step()
                 self.decode_launches += 1
-                self.pin_nxt[slot].copy_(out, non_blocking=True)
+                self.pin_nxt[slot][0].copy_(out, non_blocking=True)
+            else:
+                if T in graphs:
+                    graphs[T][0].replay()
+                    out_t, adv = graphs[T][1]
+                else:
+                    out_t, adv = self._spec_step(k)
+                self.decode_launches += 1
+                self.spec_launches += 1
+                self.pin_nxt[slot].copy_(out_t, non_blocking=True)
+                self.pin_adv[slot].copy_(adv, non_blocking=True)
             self.events[slot].record(stream)
 
+        t1 = self.step_ms.get(1, 1.0)
+        tk = self.step_ms.get(T, 1.0) if k else float("inf")
+        mode = "spec" if k else "plain"
+        rate = tk / t1 + 0.25 if k else 0.0       # optimistic start: speculate first
+        plain_left = probe_left = 0
+        probe_plain, probe_spec = CONFIG["spec_probe"]
+        losing = lambda: rate * t1 < tk * 1.03   # noqa: E731
+
+        queues = [deque() for _ in range(B)]
+        produced = [0] * B
         inflight = deque()
         launch(0, "first")
-        inflight.append(0)
+        inflight.append((0, "first"))
         launched = 1
+        potential = 1      # upper bound on the tokens per sequence the in-flight steps can still bring
         yielded = 0
         while yielded < N:
-            while len(inflight) <= depth and launched < N:
+            while len(inflight) <= depth and min(produced) + potential < N:
                 slot = launched % ring
-                launch(slot, "plain")
-                inflight.append(slot)
                 launched += 1
-            slot = inflight.popleft()
+                if k:
+                    if mode == "plain":
+                        plain_left -= 1
+                        if plain_left <= 0:
+                            mode, probe_left = "spec", probe_spec
+                    elif probe_left > 0:
+                        probe_left -= 1
+                        if probe_left == 0 and losing():
+                            mode, plain_left = "plain", probe_plain
+                m = mode
+                if m == "spec" and N - min(produced) - potential <= 1:
+                    m = "plain"    # one token left: the cheap step wins
+                launch(slot, m)
+                inflight.append((slot, m))
+                potential += T if m == "spec" else 1
+            slot, m = inflight.popleft()
+            potential -= T if m == "spec" else 1
             self.events[slot].synchronize()
-            yield [int(t) for t in self.pin_nxt[slot].tolist()]
-            yielded += 1
+            if m == "spec":
+                rows = self.pin_nxt[slot].tolist()          # rows[j][b]
+                adv = self.pin_adv[slot].tolist()
+                gains = []
+                for b in range(B):
+                    a = int(adv[b])
+                    queues[b].extend(int(rows[j][b]) for j in range(a))
+                    produced[b] += a
+                    if produced[b] < N:
+                        gains.append(a)
+                if gains:
+                    rate = 0.75 * rate + 0.25 * min(gains)
+                    self.spec_tokens += min(gains)
+                    if probe_left == 0 and mode == "spec" and losing():
+                        mode, plain_left = "plain", probe_plain
+            else:
+                for b, t in enumerate(self.pin_nxt[slot][0].tolist()):
+                    queues[b].append(int(t))
+                    produced[b] += 1
+            while yielded < N and all(queues):
+                yield [q.popleft() for q in queues]
+                yielded += 1

@@ -37,6 +37,8 @@ SIGNATURES = {
     "qwen_argmax_extract": (_i, [_p, _i, _p, _p]),
     "qwen_embed": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _ll, _i, _p]),
     "qwen_decode_finish": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _ll, _i, _p]),
+    "qwen_spec_draft": (_i, [_p, _p, _i, _i, _i, _i, _p, _p]),
+    "qwen_spec_accept": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _ll, _i, _p]),
     "qwen_tile_weight": (_i, [_p, _p, _ll, _i, _i, _p]),
     "qwen_init_weight": (_i, [_p, _ll, _i, _i, _i, _pi, _pi, _i, ctypes.c_ulonglong, _f, _p]),
 }

@@ -466,6 +466,30 @@ def decode_finish(keys, nxt, hist, pos, s_buf, ntarget, w: TiledWeight, h, psq) 
               w.K, _stream())
 
 
+def spec_draft(hist: torch.Tensor, pos: torch.Tensor, k: int, n: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prompt-lookup drafts ``[B, k+1]`` = ``[hist[L-1], draft...]`` (``engine/engine.py:955-977``)."""
+    _gpu(hist, pos, out)
+    B, cap = hist.shape
+    assert hist.dtype == torch.int64 and hist.is_contiguous()
+    assert pos.dtype == torch.int32 and pos.numel() == B and pos.is_contiguous()
+    if out is None:
+        out = torch.empty((B, k + 1), dtype=torch.int64, device=hist.device)
+    assert out.shape == (B, k + 1) and out.dtype == torch.int64 and out.is_contiguous()
+    _lib.call("qwen_spec_draft", hist.data_ptr(), pos.data_ptr(), B, cap, int(k), int(n), out.data_ptr(), _stream())
+    return out
+
+
+def spec_accept(nxt, tok, hist, pos, s_buf, ntarget, w: TiledWeight, h, psq, out_t, adv) -> None:
+    """Verify-step acceptance (``engine/engine.py:994-1003``): history scatter, position advance,
+    ``out_t [T, B]`` / ``adv [B]`` for the host, and the next plain step's input row."""
+    B, cap = hist.shape
+    T = tok.shape[1]
+    assert nxt.numel() == B * T and tok.shape == (B, T) and out_t.shape == (T, B) and adv.numel() == B
+    _lib.call("qwen_spec_accept", nxt.data_ptr(), tok.data_ptr(), hist.data_ptr(), pos.data_ptr(), s_buf.data_ptr(),
+              ntarget.data_ptr(), B, cap, T, out_t.data_ptr(), adv.data_ptr(), w.data.data_ptr(), h.data_ptr(),
+              psq.data_ptr(), w.N, w.K, _stream())
+
+
 def embed(tok: torch.Tensor, w: TiledWeight, out: torch.Tensor | None = None,
           psq_out: torch.Tensor | None = None) -> torch.Tensor:
     """``F.embedding(tok, W)`` from the tiled tied table; ``tok`` int64 ``[M]``."""
