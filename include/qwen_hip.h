@@ -76,6 +76,22 @@ int qwen_attn_decode_fused(const void* qkv, const void* q_norm_w, const void* k_
                            void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
                            int P, float eps, float scale, int num_splits, int waves, hipStream_t stream);
 
+/* Workspace bytes for qwen_attn_decode_mfma with the given split count (0 for num_splits == 1):
+ * one arrival counter per (sequence, KV head) and the split partials. Same life cycle as
+ * qwen_attn_workspace_bytes: zero before first use, every launch re-arms the counters. */
+long long qwen_attn_mfma_workspace_bytes(int B, int T, int Nkv, int num_splits);
+
+/* qwen_attn_decode_fused on the matrix cores: same operator, arguments and effects, for
+ * 1 <= T <= 8 and 1 <= num_splits <= 8. One workgroup per (sequence, KV head, split) serves
+ * all T * 4 query rows of the KV head (each cache byte read once per launch); QK^T and PV run
+ * on v_mfma_f32_16x16x32_bf16; waves (4|8) wavefronts split each context split further.
+ * Replaces engine/kernels/rope.py:169-226 followed by engine/kernels/attention.py:278-348
+ * (the two ops of engine/engine.py:1110-1113). */
+int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                          const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                          void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
+                          int P, float eps, float scale, int num_splits, int waves, hipStream_t stream);
+
 /* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
  * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed
  * projections consume (psq_in below). No reference counterpart: it is the first

@@ -1,0 +1,462 @@
+// The decode step's QK-norm + RoPE + KV write + GQA attention on the matrix cores.
+//
+// Same operator as qwen_attn_decode_fused (attention.hip): engine/kernels/rope.py:169-226
+// followed by engine/kernels/attention.py:278-348, with the rounding points of
+// torch_ref.py:94-227 — q and the T new keys are RMS-normed (gain after the bf16 cast),
+// rotated with three bf16 roundings; scores are fp32 (q.k) * scale; the un-normalised
+// probabilities are rounded to bf16 for the PV product; row sums stay fp32; one final
+// bf16 rounding. Query t of a sequence sees key j iff j < pos + t + 1.
+//
+// Work decomposition (CDNA4): one workgroup per (sequence, KV head, context split) serves
+// all R = T * 4 query rows of that KV head (the T query tokens x the 4 query heads), so
+// each cache byte is read once for all of them. Its wavefronts split the split's keys
+// into blocks of 32. Per block and wavefront:
+//   S [16-row tiles x 32 keys] = Q K^T on v_mfma_f32_16x16x32_bf16: the A operand (Q) is
+//     staged once in LDS; the B operand (K^T) is loaded straight from the cache, lane
+//     (q, r) reading key r's 16 bytes at dims 32kt + 8q (contiguous rows of the cache);
+//   online softmax in the accumulator layout (lane (q, r) holds rows 4q..4q+3 of key r);
+//   P goes through LDS into the A layout of the PV product;
+//   V [32 keys x 128 dims] is written to LDS (288-byte rows) and read back transposed by
+//     ds_read_b64_tr_b16: in each 16-lane group, result lane L, element e comes from the
+//     address of source lane 4e + L/4, element L%4 (probed on the MI355X), so source lane
+//     s pointing at V[key0 + s/4][dim0 + 4(s%4)] yields V[key0 + e][dim0 + L] in lane L;
+//   O [rows x 128 dims] += P V on the matrix cores (8 tiles of 16 dims).
+// Wavefront results merge by log-sum-exp in LDS, splits through the last-arriving
+// workgroup (device-coherent partials, as attention.hip). The new keys are normed,
+// rotated and written to the cache by split 0's workgroup and consumed from LDS; no
+// workgroup reads a cache slot this launch writes.
+#include "common.h"
+
+namespace {
+
+constexpr int MD = 128;          // head dim
+constexpr int MG = 4;            // query heads per KV head
+constexpr int MKB = 32;          // keys per block
+constexpr int VROW = 144;        // bf16 per LDS row of V (288 B: 4-way banked transpose reads)
+constexpr int MERGE_MAX = 8;     // splits merged in one round trip by the last arriver
+constexpr float MNEG = -1e30f;
+
+typedef short mv4i16 __attribute__((ext_vector_type(4)));
+typedef unsigned mu32x4 __attribute__((ext_vector_type(4)));  // 16 bytes held as a vector (stays in VGPRs)
+typedef __attribute__((address_space(3))) mv4i16 lds_mv4i16;
+
+struct MfmaAttnParams {
+  const bf16_t* qkv;      // [B*T, (Nq+2Nkv)*D]
+  const bf16_t* qnw;      // [D]
+  const bf16_t* knw;      // [D]
+  const bf16_t* cos_tab;  // [P, D]
+  const bf16_t* sin_tab;
+  const int32_t* pos;     // [B]
+  bf16_t* kc;             // [B, Nkv, CAP, D]
+  bf16_t* vc;
+  bf16_t* out;            // [B, T, Nq*D]
+  float* part;            // [B*Nkv][S][MT*16][2 + D] split partials (S > 1)
+  unsigned* cnt;          // [B*Nkv] arrival counters (S > 1), zero between launches
+  int T, Nkv, CAP, P, S;
+  float scale, eps;
+};
+
+__device__ __forceinline__ void mstore_dev(float* q, float v) {
+  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float mload_dev(const float* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One 128-wide head held as dims (c, c + 64) by lane c of a wavefront: RMSNorm (gain after
+// the bf16 cast) and RoPE at table row `row`: bf16(bf16(y cos) + bf16(rot(y) sin)).
+__device__ __forceinline__ void mnorm_rope(float& x0, float& x1, const bf16_t* gain, const bf16_t* cos_tab,
+                                           const bf16_t* sin_tab, long long row, int c, float eps) {
+  const float ss = wave_sum(add_rn(mul_rn(x0, x0), mul_rn(x1, x1)));
+  const float rinv = 1.0f / sqrtf(ss / (float)MD + eps);
+  const float y0 = rbf(mul_rn(bf2f(gain[c]), rbf(mul_rn(x0, rinv))));
+  const float y1 = rbf(mul_rn(bf2f(gain[c + 64]), rbf(mul_rn(x1, rinv))));
+  const bf16_t* cr = cos_tab + row * MD;
+  const bf16_t* sr = sin_tab + row * MD;
+  x0 = rbf(add_rn(rbf(mul_rn(y0, bf2f(cr[c]))), rbf(mul_rn(-y1, bf2f(sr[c])))));
+  x1 = rbf(add_rn(rbf(mul_rn(y1, bf2f(cr[c + 64]))), rbf(mul_rn(y0, bf2f(sr[c + 64])))));
+}
+
+template <int MT, int WPG>
+struct MfmaSmem {
+  bf16_t q[MT * 16][MD];                 // normed + rotated queries (rows past R are zero)
+  bf16_t knew[MKB][MD];                  // the new keys (rows past T are zero)
+  bf16_t vnew[MKB][VROW];                // the new values (rows past T are zero)
+  union {
+    struct {
+      bf16_t v[WPG][MKB][VROW];          // each wavefront's current V block
+      bf16_t pm[WPG][MT * 16][MKB];      // each wavefront's P tile
+    } blk;
+    float merge[WPG][MT * 16][2 + MD];   // per-wavefront (m, l, O) for the merge
+  } u;
+  unsigned last;
+};
+
+template <int MT, int WPG>
+__global__ void __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(1, 2)))
+attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most two wavefronts per SIMD
+  __shared__ MfmaSmem<MT, WPG> sm;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qq = lane >> 4, rr = lane & 15;
+  const long long bh = blockIdx.x;
+  const long long b = bh / p.Nkv;
+  const int kvh = (int)(bh - b * p.Nkv);
+  const int split = blockIdx.y;
+  const int T = p.T;
+  const int R = T * MG;
+  const int Nq = p.Nkv * MG;
+  const int nheads = Nq + 2 * p.Nkv;
+  const long long pos0 = p.pos[b];
+  const int nold = (int)min((long long)p.CAP, max(0ll, pos0));  // cached keys [0, nold)
+  const bf16_t* kbase = p.kc + bh * p.CAP * MD;
+  const bf16_t* vbase = p.vc + bh * p.CAP * MD;
+
+  // ---- prologue: q rows and new keys, normed + rotated (one row per wavefront at a time)
+  for (int r = wave; r < MT * 16; r += WPG) {
+    float x0 = 0.f, x1 = 0.f;
+    if (r < R) {
+      const int t = r / MG, g = r - t * MG;
+      const bf16_t* qr = p.qkv + ((b * T + t) * nheads + (long long)(kvh * MG + g)) * MD;
+      x0 = bf2f(qr[lane]);
+      x1 = bf2f(qr[lane + 64]);
+      mnorm_rope(x0, x1, p.qnw, p.cos_tab, p.sin_tab, min((long long)p.P - 1, max(0ll, pos0 + t)), lane, p.eps);
+    }
+    sm.q[r][lane] = f2bf(x0);
+    sm.q[r][lane + 64] = f2bf(x1);
+  }
+  for (int t = wave; t < MKB; t += WPG) {
+    float k0 = 0.f, k1 = 0.f;
+    bf16_t v0 = 0, v1 = 0;
+    if (t < T) {
+      const bf16_t* row = p.qkv + (b * T + t) * nheads * MD;
+      const bf16_t* kr = row + (long long)(Nq + kvh) * MD;
+      const bf16_t* vr = row + (long long)(Nq + p.Nkv + kvh) * MD;
+      k0 = bf2f(kr[lane]);
+      k1 = bf2f(kr[lane + 64]);
+      v0 = vr[lane];
+      v1 = vr[lane + 64];
+      mnorm_rope(k0, k1, p.knw, p.cos_tab, p.sin_tab, min((long long)p.P - 1, max(0ll, pos0 + t)), lane, p.eps);
+      const long long slot = pos0 + t;
+      if (split == 0 && slot >= 0 && slot < p.CAP) {  // one workgroup per (sequence, KV head) writes the cache
+        bf16_t* kd = p.kc + (bh * p.CAP + slot) * MD;
+        bf16_t* vd = p.vc + (bh * p.CAP + slot) * MD;
+        kd[lane] = f2bf(k0);
+        kd[lane + 64] = f2bf(k1);
+        vd[lane] = v0;
+        vd[lane + 64] = v1;
+      }
+    }
+    sm.knew[t][lane] = f2bf(k0);
+    sm.knew[t][lane + 64] = f2bf(k1);
+    sm.vnew[t][lane] = v0;
+    sm.vnew[t][lane + 64] = v1;
+  }
+  __syncthreads();
+
+  // Q A-operand fragments: lane (q, r) holds Q[16 mt + r][32 kt + 8 q .. +8].
+  bf16x8_t qa[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+      qa[mt][kt] = as_bf16x8(*reinterpret_cast<const uint4*>(&sm.q[mt * 16 + rr][32 * kt + 8 * qq]));
+
+  // ---- key partition: old keys in blocks of 32 over (split, wavefront); the new-key
+  // block goes to the last wavefront of the last split.
+  const int nblk = (nold + MKB - 1) / MKB;
+  const int per_split = (nblk + p.S - 1) / p.S;
+  const int sb0 = min(nblk, split * per_split), sb1 = min(nblk, sb0 + per_split);
+  const int per_wave = (sb1 - sb0 + WPG - 1) / WPG;
+  const int wb0 = min(sb1, sb0 + wave * per_wave), wb1 = min(sb1, wb0 + per_wave);
+  const bool takes_new = split == p.S - 1 && wave == WPG - 1;
+
+  float m[MT][4], l[MT][4];
+  f32x4_t o[MT][8];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m[mt][i] = MNEG; l[mt][i] = 0.f; }
+#pragma unroll
+    for (int nd = 0; nd < 8; ++nd) o[mt][nd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  bf16_t* vl = &sm.u.blk.v[wave][0][0];
+  bf16_t* pl = &sm.u.blk.pm[wave][0][0];
+
+  // Loads of one cached block (keys past nold re-read key 0, a valid row, and are masked).
+  mu32x4 kf[2][4], vr[8];
+  auto load_block = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int key = kb + 16 * nt + rr;
+      const bf16_t* kp = kbase + (long long)(key < nold ? key : 0) * MD + 8 * qq;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) kf[nt][kt] = *reinterpret_cast<const mu32x4*>(kp + 32 * kt);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = kb + 4 * i + qq;
+      vr[i] = *reinterpret_cast<const mu32x4*>(vbase + (long long)(key < nold ? key : 0) * MD + 8 * rr);
+    }
+  };
+
+  // One block: S = Q K^T, online softmax, O = O * alpha + P V. `vsrc` holds the block's V
+  // rows in LDS (VROW stride); `visible(nt, row)` masks keys.
+  auto process = [&](const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
+    f32x4_t s[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        s[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[mt][kt], __builtin_bit_cast(bf16x8_t, kf[nt][kt]), s[mt][nt], 0, 0, 0);
+      }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float alpha[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mt * 16 + 4 * qq + i;
+        float sv[2];
+        bool vis[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          vis[nt] = visible(nt, row);
+          sv[nt] = vis[nt] ? s[mt][nt][i] * p.scale : MNEG;
+        }
+        float mx = fmaxf(sv[0], sv[1]);
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+        const float mn = fmaxf(m[mt][i], mx);
+        alpha[i] = __expf(m[mt][i] - mn);
+        float psum = 0.f;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const float pr = vis[nt] ? __expf(sv[nt] - mn) : 0.f;
+          psum += pr;
+          pl[(mt * 16 + 4 * qq + i) * MKB + 16 * nt + rr] = f2bf(pr);  // P rounded to bf16 for PV
+        }
+        l[mt][i] = l[mt][i] * alpha[i] + psum;
+        m[mt][i] = mn;
+      }
+      if (__any(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
+#pragma unroll
+        for (int nd = 0; nd < 8; ++nd)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[mt][nd][i] *= alpha[i];
+      }
+    }
+    // P in the A layout: lane (q, r) takes P[16 mt + r][8 q .. +8]. The LDS round trip stays
+    // within the wavefront (LDS instructions complete in issue order); the signal fence keeps
+    // the compiler from moving these reads above the other lanes' writes.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    bf16x8_t pa[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pa[mt] = as_bf16x8(*reinterpret_cast<const uint4*>(pl + (mt * 16 + rr) * MKB + 8 * qq));
+    // V^T B operand by transpose reads: source lane s -> V[8q + s/4 (+4)][16 nd + 4 (s%4)].
+    const bf16_t* vs = vsrc + (8 * qq + (rr >> 2)) * VROW + 4 * (rr & 3);
+#pragma unroll
+    for (int nd = 0; nd < 8; ++nd) {
+      const mv4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_mv4i16*)(vs + 16 * nd));
+      const mv4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_mv4i16*)(vs + 4 * VROW + 16 * nd));
+      const uint4 vv = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                  __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        o[mt][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[mt], as_bf16x8(vv), o[mt][nd], 0, 0, 0);
+    }
+  };
+
+  if (wb0 < wb1) load_block(wb0 * MKB);
+  for (int blk = wb0; blk < wb1; ++blk) {
+    const int kb = blk * MKB;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the previous block's transpose reads come first
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<mu32x4*>(vl + (4 * i + qq) * VROW + 8 * rr) = vr[i];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    process(vl, [&](int nt, int row) { return kb + 16 * nt + rr < nold && row < R; });
+    if (blk + 1 < wb1) load_block((blk + 1) * MKB);
+  }
+  if (takes_new) {  // the T new keys, from LDS; query row r (token r / 4) sees new key j iff j <= r / 4
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        kf[nt][kt] = *reinterpret_cast<const mu32x4*>(&sm.knew[16 * nt + rr][32 * kt + 8 * qq]);
+    process(&sm.vnew[0][0], [&](int nt, int row) {
+      const int j = 16 * nt + rr;
+      return j < T && row < R && j <= row / MG;
+    });
+  }
+
+  // ---- merge: row sums over the 16 lanes of a group, then wavefronts in order through LDS
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = l[mt][i];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      l[mt][i] = v;
+    }
+  __syncthreads();  // every wavefront is done with its V / P tiles (the merge area aliases them)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* mrow = sm.u.merge[wave][mt * 16 + 4 * qq + i];
+      if (rr == 0) {
+        mrow[0] = m[mt][i];
+        mrow[1] = l[mt][i];
+      }
+#pragma unroll
+      for (int nd = 0; nd < 8; ++nd) mrow[2 + 16 * nd + rr] = o[mt][nd][i];
+    }
+  __syncthreads();
+
+  // Thread -> (row, 8-dim chunk) items of the R x 128 result.
+  constexpr int NT = 64 * WPG;
+  const int items = R * (MD / 8);
+  float* mine = p.part + ((bh * p.S + split) * (MT * 16)) * (2 + MD);
+  for (int it = threadIdx.x; it < items; it += NT) {
+    const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
+    float M = MNEG;
+#pragma unroll
+    for (int w = 0; w < WPG; ++w) M = fmaxf(M, sm.u.merge[w][row][0]);
+    float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < WPG; ++w) {
+      const float sc = __expf(sm.u.merge[w][row][0] - M);
+      L += sc * sm.u.merge[w][row][1];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += sc * sm.u.merge[w][row][2 + d0 + e];
+    }
+    if (p.S == 1) {
+      const int t = row / MG, g = row - t * MG;
+      float r8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r8[e] = acc[e] / L;
+      *reinterpret_cast<uint4*>(p.out + ((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d0) = pack8(r8);
+    } else {
+      float* pr = mine + (long long)row * (2 + MD);
+      if (d0 == 0) {
+        mstore_dev(pr, M);
+        mstore_dev(pr + 1, L);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mstore_dev(pr + 2 + d0 + e, acc[e]);
+    }
+  }
+  if (p.S == 1) return;
+
+  // ---- splits: the last-arriving workgroup merges them in split order
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(p.cnt + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.last = old == (unsigned)(p.S - 1);
+  }
+  __syncthreads();
+  if (!sm.last) return;
+  const float* all = p.part + (bh * p.S) * (MT * 16) * (2 + MD);
+  const long long sstride = (long long)(MT * 16) * (2 + MD);
+  for (int it = threadIdx.x; it < items; it += NT) {
+    const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
+    // every split's partial requested at once (S <= MERGE_MAX), merged in split order
+    float ms[MERGE_MAX], ls[MERGE_MAX], os[MERGE_MAX][8];
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX; ++j) {
+      const float* ps = all + min(j, p.S - 1) * sstride + (long long)row * (2 + MD);
+      ms[j] = mload_dev(ps);
+      ls[j] = mload_dev(ps + 1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) os[j][e] = mload_dev(ps + 2 + d0 + e);
+    }
+    float MM = MNEG;
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX; ++j)
+      if (j < p.S) MM = fmaxf(MM, ms[j]);
+    float LL = 0.f, oo[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX; ++j) {
+      if (j < p.S) {
+        const float sc = __expf(ms[j] - MM);
+        LL += sc * ls[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) oo[e] += sc * os[j][e];
+      }
+    }
+    const int t = row / MG, g = row - t * MG;
+    float r8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r8[e] = oo[e] / LL;
+    *reinterpret_cast<uint4*>(p.out + ((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d0) = pack8(r8);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(p.cnt + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+namespace {
+
+long long mfma_counter_bytes(long long rows) { return (rows * 4 + 255) / 256 * 256; }
+
+int mfma_rows(int T) { return T <= 4 ? 16 : 32; }
+
+template <int MT>
+int launch_mfma(const MfmaAttnParams& p, int B, int waves, hipStream_t stream) {
+  dim3 grid((unsigned)((long long)B * p.Nkv), p.S);
+  if (waves == 4) attn_mfma_kernel<MT, 4><<<grid, 256, 0, stream>>>(p);
+  else if (waves == 8) attn_mfma_kernel<MT, 8><<<grid, 512, 0, stream>>>(p);
+  else return QWEN_EARG;
+  QWEN_RETURN_LAUNCH();
+}
+
+}  // namespace
+
+extern "C" {
+
+long long qwen_attn_mfma_workspace_bytes(int B, int T, int Nkv, int num_splits) {
+  if (B <= 0 || T < 1 || T > 8 || Nkv <= 0 || num_splits < 1 || num_splits > MERGE_MAX) return 0;
+  if (num_splits == 1) return 0;
+  const long long bh = (long long)B * Nkv;
+  return mfma_counter_bytes(bh) + bh * num_splits * mfma_rows(T) * (2 + MD) * (long long)sizeof(float);
+}
+
+int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                          const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                          void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
+                          int P, float eps, float scale, int num_splits, int waves, hipStream_t stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !k_cache || !v_cache || !out)
+    return QWEN_ENULL;
+  if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || CAP <= 0 || P <= 0) return QWEN_EARG;
+  if (num_splits < 1 || num_splits > MERGE_MAX || (waves != 4 && waves != 8)) return QWEN_EARG;
+  if ((long long)B * Nkv > 0x7fffffffLL) return QWEN_EARG;
+  if (B == 0) return QWEN_OK;
+  const long long need = qwen_attn_mfma_workspace_bytes(B, T, Nkv, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return workspace ? QWEN_EWORKSPACE : QWEN_ENULL;
+  MfmaAttnParams p{};
+  p.qkv = (const bf16_t*)qkv;
+  p.qnw = (const bf16_t*)q_norm_w;
+  p.knw = (const bf16_t*)k_norm_w;
+  p.cos_tab = (const bf16_t*)cos_tab;
+  p.sin_tab = (const bf16_t*)sin_tab;
+  p.pos = positions;
+  p.kc = (bf16_t*)k_cache;
+  p.vc = (bf16_t*)v_cache;
+  p.out = (bf16_t*)out;
+  const long long bh = (long long)B * Nkv;
+  p.cnt = num_splits > 1 ? (unsigned*)workspace : nullptr;
+  p.part = num_splits > 1 ? (float*)((char*)workspace + mfma_counter_bytes(bh)) : nullptr;
+  p.T = T; p.Nkv = Nkv; p.CAP = CAP; p.P = P; p.S = num_splits;
+  p.scale = scale; p.eps = eps;
+  return T <= 4 ? launch_mfma<1>(p, B, waves, stream) : launch_mfma<2>(p, B, waves, stream);
+}
+
+}  // extern "C"

@@ -282,7 +282,9 @@ class Engine:
         key = (B, T)
         if key not in self.bufs:
             M, dev = B * T, self.device
-            S = ops.choose_num_splits(B, self.Nkv, self.CAP, T)
+            mfma = T <= ops.MFMA_MAX_T   # matrix-core attention for decode / verify widths
+            S = (ops.choose_mfma_splits(B, self.Nkv, self.CAP) if mfma
+                 else ops.choose_num_splits(B, self.Nkv, self.CAP, T))
             W_qkv = (self.Nq + 2 * self.Nkv) * self.D
             cfg = {
                 "qkv": ops.gemm_config(M, W_qkv, self.H),
@@ -311,9 +313,11 @@ class Engine:
                 "out_t": torch.zeros((T, B), dtype=torch.int64, device=dev),    # verify-step tokens, [T, B]
                 "adv": torch.zeros((B,), dtype=torch.int64, device=dev),        # accepted tokens per row
                 "keys": ops.argmax_keys(M, dev),
+                "attn_mfma": mfma,
                 "splits": S,
-                "attn_waves": ops.attn_waves(B, T),
-                "attn_ws": ops.attn_workspace(B, T, self.Nq, self.Nkv, self.D, S, dev),
+                "attn_waves": ops.MFMA_WAVES if mfma else ops.attn_waves(B, T),
+                "attn_ws": (ops.attn_mfma_workspace(B, T, self.Nkv, S, dev) if mfma
+                            else ops.attn_workspace(B, T, self.Nq, self.Nkv, self.D, S, dev)),
                 "gemm_ws": ops.linear_workspace(ws, dev),
                 "cfg": cfg,
                 "gemv": gemv,
@@ -354,9 +358,9 @@ class Engine:
             else:
                 ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq,
                                  workspace=ws)
-            ops.attn_decode_fused(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
-                                  self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
-                                  workspace=b["attn_ws"], waves=b["attn_waves"])
+            attn = ops.attn_decode_mfma if b["attn_mfma"] else ops.attn_decode_fused
+            attn(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T, self.k_cache[l],
+                 self.v_cache[l], self.scale, b["splits"], out=a, workspace=b["attn_ws"], waves=b["attn_waves"])
             if gc is not None:
                 ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
                 ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, cfg=gc["gu"])

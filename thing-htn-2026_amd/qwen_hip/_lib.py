@@ -28,6 +28,9 @@ SIGNATURES = {
     "qwen_attn_decode": (_i, [_p, _p, _p, _p, _i, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p]),
     "qwen_attn_decode_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _i, _f,
                                     _f, _i, _i, _p]),
+    "qwen_attn_mfma_workspace_bytes": (_ll, [_i, _i, _i, _i]),
+    "qwen_attn_decode_mfma": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _i, _f,
+                                   _f, _i, _i, _p]),
     "qwen_sumsq16": (_i, [_p, _p, _i, _i, _p]),
     "qwen_linear_workspace_bytes": (_ll, [_i, _i, _i, _i]),
     "qwen_linear": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _i, _p, _ll, _p]),

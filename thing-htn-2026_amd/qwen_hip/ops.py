@@ -207,6 +207,61 @@ def attn_decode_fused(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions,
     return o
 
 
+MFMA_MAX_T = 8
+MFMA_MAX_SPLITS = 8
+MFMA_WAVES = 8
+
+
+def choose_mfma_splits(B: int, Nkv: int, cap: int) -> int:
+    """Context splits of ``attn_decode_mfma`` for a decode shape: about 256 workgroups (one
+    per CU, each serving every query row of its KV head), at most 8, at least 128 cache slots
+    per split. Measured on MI355X at B = 1, 4, 8, 16, 32 (T = 1 and 5): the best split count
+    was within 5% of this choice at every shape."""
+    want = max(1, 256 // max(1, B * Nkv))
+    return max(1, min(want, MFMA_MAX_SPLITS, max(1, cap // 128)))
+
+
+def attn_mfma_workspace(B, T, Nkv, num_splits, device) -> torch.Tensor:
+    """Zeroed workspace of ``attn_decode_mfma`` (split partials + re-armed arrival counters)."""
+    return torch.zeros(max(16, _lib.query("qwen_attn_mfma_workspace_bytes", B, T, Nkv, num_splits)),
+                       dtype=torch.uint8, device=device)
+
+
+def attn_decode_mfma(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, T, k_cache, v_cache, scale,
+                     num_splits, *, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                     waves: int = 4) -> torch.Tensor:
+    """``attn_decode_fused`` on the matrix cores (``T <= 8``, ``num_splits <= 8``).
+
+    Same operator as the reference's ``qk_norm_rope_cache`` + ``attn_decode``
+    (``rope.py:169-226``, ``attention.py:278-348``); one workgroup per (sequence,
+    KV head, split) serves the ``4 T`` query rows of a KV head.
+    """
+    _gpu(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache)
+    B, Nkv, CAP, D = k_cache.shape
+    M, W = qkv.shape
+    assert D == 128 and W % D == 0 and W // D > 2 * Nkv, f"qkv width {W} vs {Nkv} KV heads of {D}"
+    Nq = W // D - 2 * Nkv
+    assert Nq == 4 * Nkv and M == B * T and 1 <= T <= MFMA_MAX_T, "G = 4, rows = B*T, T <= 8"
+    assert qkv.dtype == BF16 and qkv.is_contiguous()
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and v_cache.shape == k_cache.shape
+    assert k_cache.dtype == BF16 and v_cache.dtype == BF16
+    assert q_norm_w.numel() == D and k_norm_w.numel() == D and q_norm_w.is_contiguous() and k_norm_w.is_contiguous()
+    assert cos_tab.dim() == 2 and cos_tab.shape[1] == D and cos_tab.is_contiguous() and sin_tab.shape == cos_tab.shape
+    assert cos_tab.dtype == BF16 and sin_tab.dtype == BF16
+    assert positions.dtype == torch.int32 and positions.numel() == B and positions.is_contiguous()
+    S = int(num_splits)
+    assert 1 <= S <= MFMA_MAX_SPLITS and waves in (4, 8)
+    if workspace is None:
+        workspace = attn_mfma_workspace(B, T, Nkv, S, qkv.device)
+    o = out if out is not None else torch.empty((B, T, Nq * D), dtype=BF16, device=qkv.device)
+    assert o.is_contiguous() and o.numel() == B * T * Nq * D and o.dtype == BF16
+    _lib.call("qwen_attn_decode_mfma", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+              cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              o.data_ptr(), workspace.data_ptr(), workspace.numel(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0],
+              float(eps), float(scale), S, int(waves), _stream())
+    return o
+
+
 # ------------------------------------------------------- weights + GEMMs
 
 class TiledWeight:
