@@ -154,7 +154,7 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3, T=1):
     M = B * T
     bytes_launch = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
     name = ("gemv_kernel<%d, %d, true, 2>" % (M, b["gemv_cfg"]["gu"][1]) if b["gemv"]
-            else "skinny_gemm_kernel<%d, %d, %d, true, 2>" % ((2 if M > 16 else 1), cfg[0], cfg[1]))
+            else ops.gemm_kernel_name(M, cfg, True, ops.EPI_SWIGLU))
     return avg_s, bytes_launch, name
 
 

@@ -116,6 +116,18 @@ int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int
                 const float* psq_in, float eps, const void* residual, float* psq_out, int epi, int ntw, int waves,
                 int ks, void* workspace, long long workspace_bytes, hipStream_t stream);
 
+/* qwen_linear for 1 <= M <= 32 with the rectangle decomposition: the (unit of 16*ntw weight
+ * rows, k-step of 32) plane is cut into gn x gk equal rectangles, one workgroup of wpg (8|16)
+ * wavefronts each; a workgroup stages its k-range of the (normed) activations in LDS once and
+ * streams its rectangle's weight tiles. ntw = 2 exactly for the SwiGLU pair epilogue (epi 2),
+ * else 1. Same operands, epilogues and rounding as qwen_linear; with gk > 1 the workspace is
+ * qwen_linear_workspace_bytes(M, N, ntw, gk) bytes (counters re-armed by every launch).
+ * Replaces engine/kernels/gemm_fused.py:136-173 (the fused projections of engine/engine.py:1103-1118). */
+int qwen_linear_rect(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out,
+                     const void* norm_w, const float* psq_in, float eps, const void* residual, float* psq_out,
+                     int epi, int ntw, int wpg, int gn, int gk, void* workspace, long long workspace_bytes,
+                     hipStream_t stream);
+
 /* Dynamic LDS bytes of a qwen_gemv launch shape (0 = unsupported shape). */
 long long qwen_gemv_lds_bytes(int M, int N, int K, int grid, int waves, int epi);
 

@@ -312,15 +312,39 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
   old = __shfl(old, 0, 64);
   if (old != (unsigned)(pieces - 1)) return;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // Pieces are requested FS_BATCH at a time (one round trip per batch rather than per
+  // piece) and summed in slot order.
+  constexpr int FS_BATCH = MT * NTW >= 8 ? 1 : 8 / (MT * NTW);  // at most 32 VGPRs in flight
+  f32x4_t sum[MT][NTW];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-      f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      for (int j = 0; j < pieces; ++j)
-        s += (j == slot) ? acc[mt][nt] : load_dev(base + ((size_t)(j * MT + mt) * NTW + nt) * 64);
-      acc[mt][nt] = s;
+    for (int nt = 0; nt < NTW; ++nt) sum[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < pieces; j0 += FS_BATCH) {
+    f32x4_t v[FS_BATCH][MT][NTW];
+#pragma unroll
+    for (int jj = 0; jj < FS_BATCH; ++jj) {
+      const int j = min(j0 + jj, pieces - 1);  // past the end: a valid piece, not added
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) v[jj][mt][nt] = load_dev(base + ((size_t)(j * MT + mt) * NTW + nt) * 64);
     }
+#pragma unroll
+    for (int jj = 0; jj < FS_BATCH; ++jj) {
+      const int j = j0 + jj;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          if (j < pieces) sum[mt][nt] += (j == slot) ? acc[mt][nt] : v[jj][mt][nt];
+        }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = sum[mt][nt];
   if (lane == 0) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   epilogue<MT, NTW, EPI>(p, acc, unit, lane);
 }
@@ -461,6 +485,247 @@ __global__ void __launch_bounds__(64 * SK_WAVES) sk_gemm_kernel(GemmParams p) {
   }
 }
 
+// Rectangle decomposition with the A operand staged in LDS (M <= 32 rows).
+//
+// The (unit, k-step) plane -- units of 16*NTW weight rows, k-steps of 32 -- is
+// cut into GN x GK rectangles (gridDim.x = GN*GK, normally the CU count), all
+// the same size to within one unit (k-ranges are equal), so every CU streams
+// the same weight bytes. Workgroup (gn, gk) stages its k-range of the A operand,
+// x[0:M, 32*k0 : 32*k1], in LDS -- with NORM the RMSNorm is applied here, once
+// per element -- then its WPG wavefronts stream equal contiguous pieces of the
+// rectangle's tiles in unit-major order, reading A fragments from LDS (one
+// activation read per workgroup instead of one per wavefront and tile).
+//
+// Staging is one straight-line round: wavefront w stages rows w and w + WPG
+// (each lane up to RECT_CPL 16-byte chunks per row) and, with NORM, derives those
+// rows' RMSNorm factors itself from the producer's per-16-column partial sums, so
+// no barrier separates statistics and staging. Its loads are issued before the
+// first weight batches, so the staging wait is one activation round trip while
+// the weights are already in flight. Staged rows hold only the M real rows (no
+// padding): 16-byte chunk j of row m sits at chunk j ^ (m % 16) of its row, which
+// keeps both the staging writes and the A-fragment reads (16 rows x one chunk
+// each) free of bank conflicts; rows past M read as zero.
+//
+// A piece is at most one unit long (the host checks units per rectangle <= WPG),
+// so it touches at most two units: the first unit's sums are parked in registers
+// when the second starts. Wavefront partials meet in LDS in wavefront order; with
+// GK > 1 the GK rectangles of one unit column meet in finish_split (pieces in k
+// order).
+constexpr int RECT_LDS_MAX = 160 * 1024;
+constexpr int RECT_RPW = 2;   // staged rows per wavefront (M <= 2 * WPG)
+constexpr int RECT_CPL = 5;   // staged chunks per lane and row (k-range <= 80 k-steps)
+constexpr int RECT_PPL = 4;   // RMSNorm partials per lane and row (K <= 4096 with NORM)
+
+template <int MT, int NTW, int WPG, bool NORM, int EPI>
+__global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int GN, int GK) {
+  constexpr int U = 4 / NTW;  // tiles per batch (4 KB of weights); two batches in flight per wavefront
+  extern __shared__ __align__(16) unsigned char rect_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int NU = p.N / (16 * NTW);
+  const int KT = p.K >> 5;
+  const int gn = blockIdx.x / GK, gk = blockIdx.x - (blockIdx.x / GK) * GK;
+  const int u0 = (int)((long long)NU * gn / GN), u1 = (int)((long long)NU * (gn + 1) / GN);
+  const int k0 = (int)((long long)KT * gk / GK), k1 = (int)((long long)KT * (gk + 1) / GK);
+  const int kc = k1 - k0, nun = u1 - u0, total = nun * kc;
+  const int t0 = (int)((long long)total * wave / WPG), t1 = (int)((long long)total * (wave + 1) / WPG);
+  const int rowe = kc * 32;  // bf16 per staged row
+  bf16_t* xs = reinterpret_cast<bf16_t*>(rect_smem);
+
+  // Tile (unit u, k-step k) of this rectangle: u in [0, nun), k in [0, kc).
+  const uint4* wt = reinterpret_cast<const uint4*>(p.w);
+  auto tile_ptr = [&](int u, int k, int nt) { return wt + ((size_t)(u0 + u) * NTW + nt) * KT * 64 + (size_t)(k0 + k) * 64 + lane; };
+  struct Batch {
+    uint4 bt[U][NTW];
+  };
+  // The wavefront's first tile (a valid tile whenever its piece is not empty).
+  const int ufirst = t0 / kc, kfirst = t0 - (t0 / kc) * kc;
+  // Issue the U tiles starting at cursor (cu, ck), the position of tile t; tiles at or past
+  // t1 re-read the rectangle's first tile (always valid; dead tiles meet a zero A operand).
+  auto issue = [&](Batch& b, int t, int cu, int ck) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      int uu = cu, kk = ck + i;
+      if (kk >= kc) { kk -= kc; ++uu; }
+      if (t + i >= t1) { uu = 0; kk = 0; }
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) b.bt[i][nt] = load_nt(tile_ptr(uu, kk, nt));
+    }
+  };
+
+  // Staging loads first (every load unconditional: rows past M and chunks past the row
+  // read row 0 / chunk 0 and are dropped), then the first two weight batches.
+  const int cpr = kc * 4;  // 16-byte chunks per staged row
+  const int nu = p.K >> 4;
+  uint4 xv[RECT_RPW][RECT_CPL], gv[RECT_CPL];
+  float pv[RECT_RPW][RECT_PPL];
+#pragma unroll
+  for (int i = 0; i < RECT_RPW; ++i) {
+    const int m = wave + i * WPG;
+    const size_t row = m < p.M ? (size_t)m : 0;
+#pragma unroll
+    for (int c = 0; c < RECT_CPL; ++c) {
+      const int j = lane + 64 * c;
+      xv[i][c] = *reinterpret_cast<const uint4*>(p.x + row * p.K + (size_t)k0 * 32 + (j < cpr ? j : 0) * 8);
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < RECT_PPL; ++u) pv[i][u] = p.psq_in[row * nu + min(lane + 64 * u, nu - 1)];
+    }
+  }
+  if constexpr (NORM) {
+    const uint4* nwp = reinterpret_cast<const uint4*>(p.nw);
+#pragma unroll
+    for (int c = 0; c < RECT_CPL; ++c) {
+      const int j = lane + 64 * c;
+      gv[c] = nwp[k0 * 4 + (j < cpr ? j : 0)];
+    }
+  }
+
+  const int nb = (t1 - t0 + U - 1) / U;
+  Batch b0, b1;
+  int ic_u = ufirst, ic_k = kfirst;  // issue cursor: tile t0 + U * (batches issued)
+  auto advance = [&](int& cu, int& ck) {
+    ck += U;
+    if (ck >= kc) { ck -= kc; ++cu; }
+  };
+  // Both prologue batches unconditionally (an empty piece re-reads the rectangle's first
+  // tile): every path then has the same loads in flight, so the compiler's waits for the
+  // staged activations and for batch 0 leave the later loads in flight.
+  issue(b0, t0, ic_u, ic_k);
+  advance(ic_u, ic_k);
+  issue(b1, t0 + U, ic_u, ic_k);
+  advance(ic_u, ic_k);
+
+  // Normalise and store the staged rows (row m: RMSNorm factor from the K/16 partials,
+  // summed lane-strided then by a fixed butterfly: identical in every workgroup).
+#pragma unroll
+  for (int i = 0; i < RECT_RPW; ++i) {
+    const int m = wave + i * WPG;
+    float rinv = 1.f;
+    if constexpr (NORM) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int u = 0; u < RECT_PPL; ++u) sacc += pv[i][u] * (lane + 64 * u < nu ? 1.f : 0.f);  // keeps every load used
+      rinv = 1.0f / sqrtf(wave_sum(sacc) / (float)p.K + p.eps);
+    }
+    if (m < p.M) {
+#pragma unroll
+      for (int c = 0; c < RECT_CPL; ++c) {
+        const int j = lane + 64 * c;
+        if (j < cpr) {
+          uint4 v = xv[i][c];
+          if constexpr (NORM) {
+            float f[8], gg[8], o[8];
+            unpack8(v, f);
+            unpack8(gv[c], gg);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = mul_rn(gg[e], rbf(mul_rn(f[e], rinv)));
+            v = pack8(o);
+          }
+          *reinterpret_cast<uint4*>(xs + m * rowe + (j ^ (m & 15)) * 8) = v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // A-fragment rows of this lane: rows past M read row 0's slot and are zeroed.
+  int arow[MT];
+  bool aok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    aok[mt] = 16 * mt + r < p.M;
+    arow[mt] = aok[mt] ? 16 * mt + r : 0;
+  }
+
+  f32x4_t acc[MT][NTW], saved[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = saved[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int cc_u = ufirst, cc_k = kfirst;  // consume cursor
+  int ucur = ufirst;                             // unit being accumulated (wave-uniform)
+  // Branch-free: a dead tile (past t1) meets a zero A operand, and the switch to the second
+  // unit parks the sums with selects.
+  auto consume = [&](const Batch& b, int t) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      int uu = cc_u, kk = cc_k + i;
+      if (kk >= kc) { kk -= kc; ++uu; }
+      const bool live = t + i < t1;
+      const bool sw = live && uu != ucur;
+      ucur = sw ? uu : ucur;
+      kk = live ? kk : 0;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          saved[mt][nt] = sw ? acc[mt][nt] : saved[mt][nt];
+          acc[mt][nt] = sw ? f32x4_t{0.f, 0.f, 0.f, 0.f} : acc[mt][nt];
+        }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        uint4 araw = *reinterpret_cast<const uint4*>(xs + arow[mt] * rowe + (((kk * 4 + q) ^ (arow[mt] & 15)) * 8));
+        if (!live || !aok[mt]) araw = make_uint4(0, 0, 0, 0);
+        const bf16x8_t a = as_bf16x8(araw);
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b.bt[i][nt]), acc[mt][nt], 0, 0, 0);
+      }
+    }
+    advance(cc_u, cc_k);
+  };
+  int j = 0;
+  for (; j + 3 < nb; j += 2) {  // batches j .. j+3 exist
+    consume(b0, t0 + j * U);
+    issue(b0, t0 + (j + 2) * U, ic_u, ic_k);
+    advance(ic_u, ic_k);
+    consume(b1, t0 + (j + 1) * U);
+    issue(b1, t0 + (j + 3) * U, ic_u, ic_k);
+    advance(ic_u, ic_k);
+  }
+  if (j < nb) consume(b0, t0 + j * U);
+  if (j + 2 < nb) issue(b0, t0 + (j + 2) * U, ic_u, ic_k);
+  if (j + 1 < nb) consume(b1, t0 + (j + 1) * U);
+  if (j + 2 < nb) consume(b0, t0 + (j + 2) * U);
+
+  // Wavefront partials -> LDS ([wave][slot][mt][nt][lane], aliasing the staged A), then per unit.
+  __syncthreads();
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(rect_smem);
+  if (t0 < t1) {
+    const bool two = (t1 - 1) / kc > ufirst;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        red[(((wave * 2 + 0) * MT + mt) * NTW + nt) * 64 + lane] = two ? saved[mt][nt] : acc[mt][nt];
+        if (two) red[(((wave * 2 + 1) * MT + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
+      }
+  }
+  __syncthreads();
+  for (int uu = wave; uu < nun; uu += WPG) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < WPG; ++w) {
+      const int a0 = (int)((long long)total * w / WPG), a1 = (int)((long long)total * (w + 1) / WPG);
+      if (a0 >= a1) continue;
+      const int wf = a0 / kc, wl = (a1 - 1) / kc;
+      if (uu < wf || uu > wl) continue;
+      const int slot = uu - wf;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] += red[(((w * 2 + slot) * MT + mt) * NTW + nt) * 64 + lane];
+    }
+    if (GK > 1) finish_split<MT, NTW, EPI>(p, acc, u0 + uu, gk, GK, lane);
+    else epilogue<MT, NTW, EPI>(p, acc, u0 + uu, lane);
+  }
+}
+
 // token[m] = index held in a packed argmax key; the key is re-armed to zero.
 __global__ void __launch_bounds__(64) argmax_extract_kernel(unsigned long long* __restrict__ amax, int M,
                                                             int64_t* __restrict__ out) {
@@ -544,6 +809,68 @@ int dispatch(const GemmParams& p, int grid, int mt, int ntw, int wpg, hipStream_
   return QWEN_EARG;
 }
 
+// Dynamic LDS of a rectangle launch: the M staged rows of a k-range, or the wavefront
+// partials that later alias them, whichever is larger.
+long long rect_lds_bytes(int M, int K, int ntw, int wpg, int gk) {
+  const long long MT = M > 16 ? 2 : 1;
+  const long long kc = (K / 32) / gk;
+  const long long xs = (long long)M * kc * 64;
+  const long long red = (long long)wpg * 2 * MT * ntw * 64 * 16;
+  return xs > red ? xs : red;
+}
+
+// A rectangle launch applies when every rectangle holds at least one unit and at most wpg
+// units (a wavefront's piece touches at most two), the k-ranges are equal multiples of four
+// k-steps of at most 4 * RECT_CPL * 16 / 4 (one staging round), every row has a staging
+// wavefront, NORM rows have at most 64 * RECT_PPL partials, and the LDS fits.
+bool rect_fits(int M, int N, int K, int ntw, int wpg, int gn, int gk, bool norm) {
+  if (M < 1 || M > 32 || K % 32 != 0 || (ntw != 1 && ntw != 2) || (wpg != 8 && wpg != 16)) return false;
+  if (N % (16 * ntw) != 0 || gn < 1 || gk < 1) return false;
+  const long long NU = N / (16 * ntw), KT = K / 32;
+  if (gn > NU || KT % (4 * gk) != 0) return false;
+  const long long kc = KT / gk;
+  if (kc * 4 > 64 * RECT_CPL) return false;
+  if (M > RECT_RPW * wpg) return false;
+  if (norm && K / 16 > 64 * RECT_PPL) return false;
+  if ((NU + gn - 1) / gn > wpg) return false;
+  if ((long long)gn * gk > 0x7fffffffLL || NU > QWEN_LINEAR_COUNTER_BYTES / 4) return false;
+  return rect_lds_bytes(M, K, ntw, wpg, gk) <= RECT_LDS_MAX;
+}
+
+template <int MT, int NTW, int WPG, bool NORM, int EPI>
+int launch_rect(const GemmParams& p, int gn, int gk, hipStream_t stream) {
+  auto kern = rect_gemm_kernel<MT, NTW, WPG, NORM, EPI>;
+  static bool attr = false;  // one-time opt-in to more than 64 KB of dynamic LDS
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, RECT_LDS_MAX) != hipSuccess)
+      return QWEN_EARG;
+    attr = true;
+  }
+  const size_t lds = (size_t)rect_lds_bytes(p.M, p.K, NTW, WPG, gk);
+  kern<<<gn * gk, 64 * WPG, lds, stream>>>(p, gn, gk);
+  QWEN_RETURN_LAUNCH();
+}
+
+template <bool NORM, int EPI>
+int dispatch_rect(const GemmParams& p, int gn, int gk, int ntw, int wpg, hipStream_t stream) {
+  const int mt = p.M > 16 ? 2 : 1;
+#define QWEN_RECT_CASE(MT_, NTW_, W_) \
+  if (mt == MT_ && ntw == NTW_ && wpg == W_) return launch_rect<MT_, NTW_, W_, NORM, EPI>(p, gn, gk, stream);
+  if constexpr (EPI != EPI_SWIGLU) {
+    QWEN_RECT_CASE(1, 1, 8)
+    QWEN_RECT_CASE(1, 1, 16)
+    QWEN_RECT_CASE(2, 1, 8)
+    QWEN_RECT_CASE(2, 1, 16)
+  } else {
+    QWEN_RECT_CASE(1, 2, 8)
+    QWEN_RECT_CASE(1, 2, 16)
+    QWEN_RECT_CASE(2, 2, 8)
+    QWEN_RECT_CASE(2, 2, 16)
+  }
+#undef QWEN_RECT_CASE
+  return QWEN_EARG;
+}
+
 int check_shape(const void* x, const void* w, int M, int N, int K, int ntw, int wpg, int ks) {
   if (!x || !w) return QWEN_ENULL;
   if (M <= 0 || M > 32 || N <= 0 || K <= 0 || K % 32 != 0) return QWEN_EARG;
@@ -613,6 +940,33 @@ int qwen_linear(const void* x, const void* w_tiled, void* out, int M, int N, int
                                       : dispatch<false, EPI_STORE>(p, grid, mt, ntw, wpg, stream);
   if (epi == EPI_RES) return norm_w ? QWEN_EARG : dispatch<false, EPI_RES>(p, grid, mt, ntw, wpg, stream);
   return norm_w ? dispatch<true, EPI_SWIGLU>(p, grid, mt, ntw, wpg, stream) : QWEN_EARG;
+}
+
+// qwen_linear with the rectangle decomposition: gn x gk workgroups of wpg wavefronts
+// (see rect_gemm_kernel). ntw = 2 for the SwiGLU pair epilogue, else 1. The workspace
+// (gk > 1) is qwen_linear_workspace_bytes(M, N, ntw, gk) bytes.
+int qwen_linear_rect(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out,
+                     const void* norm_w, const float* psq_in, float eps, const void* residual, float* psq_out,
+                     int epi, int ntw, int wpg, int gn, int gk, void* workspace, long long workspace_bytes,
+                     hipStream_t stream) {
+  if (!x || !w_tiled || !out) return QWEN_ENULL;
+  if (!rect_fits(M, N, K, ntw, wpg, gn, gk, norm_w != nullptr)) return QWEN_EARG;
+  if (epi == EPI_RES && !residual) return QWEN_ENULL;
+  if (norm_w && !psq_in) return QWEN_ENULL;
+  if (psq_out && (epi != EPI_RES || N % 16 != 0)) return QWEN_EARG;
+  if (epi < EPI_STORE || epi > EPI_SWIGLU || (epi == EPI_SWIGLU) != (ntw == 2)) return QWEN_EARG;
+  const int out_cols = epi == EPI_SWIGLU ? N / 2 : N;
+  if (ld_out < out_cols) return QWEN_EARG;
+  const long long need = gk > 1 ? qwen_linear_workspace_bytes(M, N, ntw, gk) : 0;
+  if (need > 0 && (!workspace || workspace_bytes < need)) return workspace ? QWEN_EWORKSPACE : QWEN_ENULL;
+  unsigned* cnt = gk > 1 ? (unsigned*)workspace : nullptr;
+  f32x4_t* part = gk > 1 ? (f32x4_t*)((char*)workspace + QWEN_LINEAR_COUNTER_BYTES) : nullptr;
+  GemmParams p{(const bf16_t*)x, (const bf16_t*)w_tiled, (const bf16_t*)norm_w, (const bf16_t*)residual,
+               (bf16_t*)out, nullptr, psq_in, psq_out, part, cnt, M, N, K, ld_out, gk, gk, eps};
+  if (epi == EPI_STORE) return norm_w ? dispatch_rect<true, EPI_STORE>(p, gn, gk, ntw, wpg, stream)
+                                      : dispatch_rect<false, EPI_STORE>(p, gn, gk, ntw, wpg, stream);
+  if (epi == EPI_RES) return norm_w ? QWEN_EARG : dispatch_rect<false, EPI_RES>(p, gn, gk, ntw, wpg, stream);
+  return norm_w ? dispatch_rect<true, EPI_SWIGLU>(p, gn, gk, ntw, wpg, stream) : QWEN_EARG;
 }
 
 // Final RMSNorm (norm_w) + LM head GEMM + argmax over the bf16 logits, lowest

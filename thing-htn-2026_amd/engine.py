@@ -293,7 +293,7 @@ class Engine:
                 "down": ops.gemm_config(M, self.H, self.I),
             }
             n_of = {"qkv": W_qkv, "o": self.H, "gu": 2 * self.I, "down": self.H}
-            ws = max(ops.linear_workspace_bytes(M, n_of[k], c[0], c[2]) for k, c in cfg.items())
+            ws = max(ops.gemm_workspace_bytes(M, n_of[k], c) for k, c in cfg.items())
             gemv = M <= ops.GEMV_MAX_M
             gemv_cfg = {
                 "qkv": ops.gemv_config(M, W_qkv, self.H, ops.GEPI_STORE, dev),

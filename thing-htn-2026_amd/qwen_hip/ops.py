@@ -321,17 +321,21 @@ def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
 _TUNED = {
     (6144, 2560, False): {1: (2, 8, 1), 16: (2, 8, 1), 32: (2, 4, 1)},      # QKV
     (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 32: (1, 4, 1)},      # O
-    (19456, 2560, True): {1: (2, 8, 1), 16: (2, 4, 1), 32: (4, 4, 1)},      # gate/up + SwiGLU
+    (19456, 2560, True): {1: (2, 8, 1), 16: (2, 4, 1), 32: (2, 16, 256, 1)},  # gate/up + SwiGLU (32: rectangles)
     (2560, 9728, False): {1: (1, 16, 1), 16: (1, 8, 1), 32: (2, 4, 2)},     # down
 }
 
 
-def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, int, int]:
-    """(ntw, waves, ksplit) launch shape for ``x[M, K] @ W[N, K]^T``.
+def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple:
+    """Launch shape for ``x[M, K] @ W[N, K]^T``: ``(ntw, waves, ksplit)`` for ``qwen_linear``
+    or ``(ntw, waves, gn, gk)`` for the rectangle launch ``qwen_linear_rect``.
 
     ``ksplit == 0`` selects the stream-K launch (one workgroup of 8 wavefronts
     per CU, equal weight bytes per CU). Known Qwen3-4B shapes use the measured
-    table; otherwise: 8 wavefronts per
+    table (MI355X, graph-replayed over 36 weight copies: the rectangle launch wins
+    only for gate/up at M > 16, 30.3 vs 37.6 us at M = 32; QKV's 384 and O / down's 160
+    n-tiles cannot be spread evenly over 256 CUs without a split-K merge that costs as
+    much as the imbalance); otherwise: 8 wavefronts per
     workgroup and enough workgroups (n-tile groups x k-splits) to give about
     four per CU on 256 CUs, keeping at least 4 k-steps (4 KB of weight per
     n-tile) per wavefront.
@@ -351,6 +355,26 @@ def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple[int, i
 
 def linear_workspace_bytes(M: int, N: int, ntw: int, ks: int) -> int:
     return _lib.query("qwen_linear_workspace_bytes", M, N, ntw, ks)
+
+
+def gemm_workspace_bytes(M: int, N: int, cfg) -> int:
+    """Split-K workspace bytes of a ``gemm_config`` launch shape (either form)."""
+    if len(cfg) == 4:
+        ntw, _, _, gk = cfg
+        return linear_workspace_bytes(M, N, ntw, gk) if gk > 1 else 0
+    ntw, _, ks = cfg
+    return linear_workspace_bytes(M, N, ntw, ks)
+
+
+def gemm_kernel_name(M: int, cfg, norm: bool, epi: int) -> str:
+    """Kernel symbol (as rocprofv3 prints it) that ``fused_linear`` launches for ``cfg``."""
+    mt = 2 if M > 16 else 1
+    flag = "true" if norm else "false"
+    if len(cfg) == 4:
+        return f"rect_gemm_kernel<{mt}, {cfg[0]}, {cfg[1]}, {flag}, {epi}>"
+    if cfg[2] == 0:
+        return f"sk_gemm_kernel<{mt}, {cfg[0]}, {flag}, {epi}>"
+    return f"skinny_gemm_kernel<{mt}, {cfg[0]}, {cfg[1]}, {flag}, {epi}>"
 
 
 def linear_workspace(nbytes: int, device) -> torch.Tensor:
@@ -402,15 +426,70 @@ def fused_linear(x: torch.Tensor, w: TiledWeight, cfg=None, *, norm_w=None, eps:
     if out is None:
         out = torch.empty((M, ncols), dtype=BF16, device=x.device)
     assert out.shape == (M, ncols) and out.is_contiguous()
-    ntw, waves, ks = cfg if cfg is not None else gemm_config(M, w.N, K, silu_pair)
+    if cfg is None:
+        cfg = gemm_config(M, w.N, K, silu_pair)
+    epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
+    if len(cfg) == 4:   # rectangle decomposition (ntw, waves, gn, gk)
+        ntw, waves, gn, gk = cfg
+        need = linear_workspace_bytes(M, w.N, ntw, gk) if gk > 1 else 0
+        if need and workspace is None:
+            workspace = linear_workspace(need, x.device)
+        _lib.call("qwen_linear_rect", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols,
+                  _nullable(norm_w), _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi,
+                  ntw, waves, gn, gk, _nullable(workspace), 0 if workspace is None else workspace.numel(), _stream())
+        return out
+    ntw, waves, ks = cfg
     need = linear_workspace_bytes(M, w.N, ntw, ks)
     if need and workspace is None:
         workspace = linear_workspace(need, x.device)
-    epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
     _lib.call("qwen_linear", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols, _nullable(norm_w),
               _nullable(psq_in), float(eps), _nullable(residual), _nullable(psq_out), epi, ntw, waves, ks,
               _nullable(workspace), 0 if workspace is None else workspace.numel(), _stream())
     return out
+
+
+RECT_LDS_MAX = 160 * 1024
+
+
+def rect_fits(M: int, N: int, K: int, ntw: int, waves: int, gn: int, gk: int, norm: bool = True) -> bool:
+    """Host mirror of the library's admission rule for a rectangle launch."""
+    if not (1 <= M <= 32 and K % 32 == 0 and ntw in (1, 2) and waves in (8, 16) and N % (16 * ntw) == 0):
+        return False
+    NU, KT = N // (16 * ntw), K // 32
+    if not (1 <= gn <= NU and gk >= 1 and KT % (4 * gk) == 0):
+        return False
+    kc = KT // gk
+    if kc * 4 > 64 * 5 or M > 2 * waves or (norm and K // 16 > 64 * 4) or -(-NU // gn) > waves:
+        return False
+    MT = 2 if M > 16 else 1
+    return max(M * kc * 64, waves * 2 * MT * ntw * 64 * 16) <= RECT_LDS_MAX
+
+
+def rect_config(M: int, N: int, K: int, silu_pair: bool = False, cus: int = 256, waves: int = 16,
+                norm: bool = True):
+    """(ntw, waves, gn, gk) of the rectangle launch: gn * gk = the CU count (or twice it), the
+    split of the (unit, k-step) plane whose largest rectangle is closest to the average, with a
+    small charge per k-group for the split-K partials; None if no split fits."""
+    ntw = 2 if silu_pair else 1
+    NU, KT = N // (16 * ntw), K // 32
+    MT = 2 if M > 16 else 1
+    best, best_cost = None, None
+    for mult in (1, 2):
+        G = cus * mult
+        for gk in range(1, min(KT // 4, 64) + 1):
+            if G % gk:
+                continue
+            gn = G // gk
+            if not rect_fits(M, N, K, ntw, waves, gn, gk, norm):
+                continue
+            if mult > 1 and waves == 16:   # a CU holds one 16-wavefront workgroup: two rounds
+                continue
+            imbalance = (-(-NU // gn)) * (-(-KT // gk)) / (NU * KT / G)
+            # a split-K merge (store, count, re-load) costs about a quarter of a small GEMM
+            cost = imbalance + (0.25 if gk > 1 else 0.0) + 0.02 * (mult - 1)
+            if best_cost is None or cost < best_cost - 1e-9:
+                best, best_cost = (ntw, waves, gn, gk), cost
+    return best
 
 
 GEMV_MAX_M = 2   # rows handled by the balanced row-major GEMV (qwen_gemv)
