@@ -1,11 +1,12 @@
 """Summaries of rocprofv3 CSV output for the decode engine (text only, a few KB).
 
-    python -m qwen_hip.rocprof_summary steps <run_kernel_trace.csv> [--last N]
+    python -m qwen_hip.rocprof_summary steps <run_kernel_trace.csv> [--last N] [--boundary NAME]
     python -m qwen_hip.rocprof_summary pmc <run_counter_collection.csv> --kernel SUBSTR
                                            --copy-bytes B --copies C
 
 ``steps``: decode steps are the intervals between consecutive
-``decode_finish_kernel`` dispatches (one per graph replay); prints, for the
+``decode_finish_kernel`` dispatches (one per graph replay; ``spec_accept_kernel``
+for speculative verify steps, via ``--boundary``); prints, for the
 last N steps, each kernel's launches per step, average duration and share of
 the step, and the step-to-step time.
 
@@ -36,10 +37,10 @@ def _rows(path):
         return list(csv.DictReader(f))
 
 
-def steps(path: str, last: int) -> str:
+def steps(path: str, last: int, boundary: str = "decode_finish_kernel") -> str:
     rows = _rows(path)
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    marks = [i for i, r in enumerate(rows) if "decode_finish_kernel" in r["Kernel_Name"]]
+    marks = [i for i, r in enumerate(rows) if boundary in r["Kernel_Name"]]
     if len(marks) < 2:
         return "no decode steps found"
     marks = marks[-(last + 1):]
@@ -59,7 +60,7 @@ def steps(path: str, last: int) -> str:
             shape[k] = f"{(gx // wx) * (gy // wy) * (gz // wz)} x {wx * wy * wz}"
     span = (int(rows[marks[-1]]["Start_Timestamp"]) - int(rows[marks[0]]["Start_Timestamp"])) / 1e3 / n
     busy = sum(sum(v) for v in per.values()) / n
-    out = [f"Decode steps analysed: the last {n} (between consecutive `decode_finish_kernel` dispatches); "
+    out = [f"Decode steps analysed: the last {n} (between consecutive `{boundary}` dispatches); "
            f"{sum(len(v) for v in per.values()) // n} kernels per step; step-to-step {span:.1f} us; "
            f"kernel busy time {busy:.1f} us per step.", "",
            "| share | per step | avg us | workgroups x threads | kernel |", "|---:|---:|---:|---|---|"]
@@ -102,13 +103,14 @@ def main():
     s = sub.add_parser("steps")
     s.add_argument("csv")
     s.add_argument("--last", type=int, default=32)
+    s.add_argument("--boundary", default="decode_finish_kernel")
     p = sub.add_parser("pmc")
     p.add_argument("csv")
     p.add_argument("--kernel", required=True)
     p.add_argument("--copy-bytes", type=int, required=True)
     p.add_argument("--copies", type=int, default=3)
     a = ap.parse_args()
-    print(steps(a.csv, a.last) if a.cmd == "steps" else pmc(a.csv, a.kernel, a.copy_bytes, a.copies))
+    print(steps(a.csv, a.last, a.boundary) if a.cmd == "steps" else pmc(a.csv, a.kernel, a.copy_bytes, a.copies))
 
 
 if __name__ == "__main__":
