@@ -63,18 +63,17 @@ __device__ __forceinline__ float mload_dev(const float* q) {
   return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One 128-wide head held as dims (c, c + 64) by lane c of a wavefront: RMSNorm (gain after
-// the bf16 cast) and RoPE at table row `row`: bf16(bf16(y cos) + bf16(rot(y) sin)).
-__device__ __forceinline__ void mnorm_rope(float& x0, float& x1, const bf16_t* gain, const bf16_t* cos_tab,
-                                           const bf16_t* sin_tab, long long row, int c, float eps) {
+// One 128-wide head held as dims (c, c + 64) by lane c of a wavefront (x0, x1), with the
+// gain (g0, g1) and the cos / sin table entries of its position already loaded: RMSNorm
+// (gain after the bf16 cast) and RoPE, bf16(bf16(y cos) + bf16(rot(y) sin)).
+__device__ __forceinline__ void mnorm_rope(float& x0, float& x1, float g0, float g1, float c0, float c1, float s0,
+                                           float s1, float eps) {
   const float ss = wave_sum(add_rn(mul_rn(x0, x0), mul_rn(x1, x1)));
   const float rinv = 1.0f / sqrtf(ss / (float)MD + eps);
-  const float y0 = rbf(mul_rn(bf2f(gain[c]), rbf(mul_rn(x0, rinv))));
-  const float y1 = rbf(mul_rn(bf2f(gain[c + 64]), rbf(mul_rn(x1, rinv))));
-  const bf16_t* cr = cos_tab + row * MD;
-  const bf16_t* sr = sin_tab + row * MD;
-  x0 = rbf(add_rn(rbf(mul_rn(y0, bf2f(cr[c]))), rbf(mul_rn(-y1, bf2f(sr[c])))));
-  x1 = rbf(add_rn(rbf(mul_rn(y1, bf2f(cr[c + 64]))), rbf(mul_rn(y0, bf2f(sr[c + 64])))));
+  const float y0 = rbf(mul_rn(g0, rbf(mul_rn(x0, rinv))));
+  const float y1 = rbf(mul_rn(g1, rbf(mul_rn(x1, rinv))));
+  x0 = rbf(add_rn(rbf(mul_rn(y0, c0)), rbf(mul_rn(-y1, s0))));
+  x1 = rbf(add_rn(rbf(mul_rn(y1, c1)), rbf(mul_rn(y0, s1))));
 }
 
 template <int MT, int WPG>
@@ -112,45 +111,144 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const bf16_t* kbase = p.kc + bh * p.CAP * MD;
   const bf16_t* vbase = p.vc + bh * p.CAP * MD;
 
-  // ---- prologue: q rows and new keys, normed + rotated (one row per wavefront at a time)
-  for (int r = wave; r < MT * 16; r += WPG) {
-    float x0 = 0.f, x1 = 0.f;
-    if (r < R) {
-      const int t = r / MG, g = r - t * MG;
-      const bf16_t* qr = p.qkv + ((b * T + t) * nheads + (long long)(kvh * MG + g)) * MD;
-      x0 = bf2f(qr[lane]);
-      x1 = bf2f(qr[lane + 64]);
-      mnorm_rope(x0, x1, p.qnw, p.cos_tab, p.sin_tab, min((long long)p.P - 1, max(0ll, pos0 + t)), lane, p.eps);
+  // ---- key partition: old keys in blocks of 32 over (split, wavefront); the new-key
+  // block goes to the last wavefront of the last split.
+  const int nblk = (nold + MKB - 1) / MKB;
+  const int per_split = (nblk + p.S - 1) / p.S;
+  const int sb0 = min(nblk, split * per_split), sb1 = min(nblk, sb0 + per_split);
+  const int per_wave = (sb1 - sb0 + WPG - 1) / WPG;
+  const int wb0 = min(sb1, sb0 + wave * per_wave), wb1 = min(sb1, wb0 + per_wave);
+  const bool takes_new = split == p.S - 1 && wave == WPG - 1;
+
+  // Loads of one cached block (keys past nold re-read key 0, a valid slot, and are masked).
+  // A cached block's K (B operand: lane (q, r) holds key 16 nt + r, dims 32 kt + 8 q ..)
+  // and V rows (lane (q, r) holds key 4 i + q, dims 8 r ..), read with non-temporal loads
+  // (each cached byte is read once per step; measured on MI355X: 7.0 vs 6.2 TB/s for a
+  // plain streaming read). Keys at or past this
+  // wavefront's end (or past nold) re-read slot 0, a valid row shared by all lanes, and are
+  // masked: a prefetch past the range costs no HBM traffic.
+  struct KVBlock {
+    mu32x4 k[2][4], v[8];
+  };
+  const int kend = min(nold, wb1 * MKB);
+  auto load_block = [&](KVBlock& d, int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int key = kb + 16 * nt + rr;
+      const bf16_t* kp = kbase + (long long)(key < kend ? key : 0) * MD + 8 * qq;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        d.k[nt][kt] = __builtin_nontemporal_load(reinterpret_cast<const mu32x4*>(kp + 32 * kt));
     }
-    sm.q[r][lane] = f2bf(x0);
-    sm.q[r][lane + 64] = f2bf(x1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = kb + 4 * i + qq;
+      d.v[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const mu32x4*>(vbase + (long long)(key < kend ? key : 0) * MD + 8 * rr));
+    }
+  };
+  // Blocks in flight per wavefront: two where the registers allow it without spilling (one
+  // 16-row query tile and four wavefronts: 228 VGPRs); otherwise one.
+  constexpr int DEPTH = (MT == 1 && WPG == 4) ? 2 : 1;
+  KVBlock blkA, blkB;
+
+  // ---- prologue. Every load a wavefront needs is issued first (rows clamped to valid ones,
+  // dropped later), then its first cached block, then the RMSNorm + RoPE work: one memory
+  // round trip, overlapped with the block's. Query row r (token r / 4, head r % 4) belongs
+  // to wavefront r % WPG, new key t to wavefront WPG - 1 - t % WPG.
+  constexpr int QPW = (MT * 16 + WPG - 1) / WPG;  // query rows per wavefront
+  constexpr int KPW = (8 + WPG - 1) / WPG;        // new keys per wavefront (T <= 8)
+  const bf16_t* ct = p.cos_tab;
+  const bf16_t* st = p.sin_tab;
+  auto tab_row = [&](int t) { return min((long long)p.P - 1, max(0ll, pos0 + t)) * MD; };
+  float qx[QPW][2], qcs[QPW][4], kx[KPW][2], kcs[KPW][4];
+  bf16_t kv[KPW][2];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int r = wave + i * WPG;
+    const int rc = r < R ? r : 0;
+    const int t = rc / MG, g = rc - t * MG;
+    const bf16_t* qr = p.qkv + ((b * T + t) * nheads + (long long)(kvh * MG + g)) * MD;
+    const long long tr = tab_row(t);
+    qx[i][0] = bf2f(qr[lane]);
+    qx[i][1] = bf2f(qr[lane + 64]);
+    qcs[i][0] = bf2f(ct[tr + lane]);
+    qcs[i][1] = bf2f(ct[tr + lane + 64]);
+    qcs[i][2] = bf2f(st[tr + lane]);
+    qcs[i][3] = bf2f(st[tr + lane + 64]);
   }
-  for (int t = wave; t < MKB; t += WPG) {
-    float k0 = 0.f, k1 = 0.f;
-    bf16_t v0 = 0, v1 = 0;
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    const int t = (WPG - 1 - wave) + j * WPG;
+    const int tc = t < T ? t : 0;
+    const bf16_t* row = p.qkv + (b * T + tc) * nheads * MD;
+    const bf16_t* kr = row + (long long)(Nq + kvh) * MD;
+    const bf16_t* vrow = row + (long long)(Nq + p.Nkv + kvh) * MD;
+    const long long tr = tab_row(tc);
+    kx[j][0] = bf2f(kr[lane]);
+    kx[j][1] = bf2f(kr[lane + 64]);
+    kv[j][0] = vrow[lane];
+    kv[j][1] = vrow[lane + 64];
+    kcs[j][0] = bf2f(ct[tr + lane]);
+    kcs[j][1] = bf2f(ct[tr + lane + 64]);
+    kcs[j][2] = bf2f(st[tr + lane]);
+    kcs[j][3] = bf2f(st[tr + lane + 64]);
+  }
+  const float qg0 = bf2f(p.qnw[lane]), qg1 = bf2f(p.qnw[lane + 64]);
+  const float kg0 = bf2f(p.knw[lane]), kg1 = bf2f(p.knw[lane + 64]);
+  load_block(blkA, wb0 * MKB);  // unconditional: a wavefront without blocks re-reads valid slots
+  if constexpr (DEPTH == 2) load_block(blkB, (wb0 + 1) * MKB);
+
+  // Rows past R / T are computed too (on clamped inputs) and not stored: every load stays
+  // used, so the compiler keeps them ahead of the block loads instead of sinking them into
+  // the branches (which would make the first wait also wait for the block).
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int r = wave + i * WPG;
+    float x0 = qx[i][0], x1 = qx[i][1];
+    mnorm_rope(x0, x1, qg0, qg1, qcs[i][0], qcs[i][1], qcs[i][2], qcs[i][3], p.eps);
+    if (r < R) {
+      sm.q[r][lane] = f2bf(x0);
+      sm.q[r][lane + 64] = f2bf(x1);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    const int t = (WPG - 1 - wave) + j * WPG;
+    float k0 = kx[j][0], k1 = kx[j][1];
+    mnorm_rope(k0, k1, kg0, kg1, kcs[j][0], kcs[j][1], kcs[j][2], kcs[j][3], p.eps);
     if (t < T) {
-      const bf16_t* row = p.qkv + (b * T + t) * nheads * MD;
-      const bf16_t* kr = row + (long long)(Nq + kvh) * MD;
-      const bf16_t* vr = row + (long long)(Nq + p.Nkv + kvh) * MD;
-      k0 = bf2f(kr[lane]);
-      k1 = bf2f(kr[lane + 64]);
-      v0 = vr[lane];
-      v1 = vr[lane + 64];
-      mnorm_rope(k0, k1, p.knw, p.cos_tab, p.sin_tab, min((long long)p.P - 1, max(0ll, pos0 + t)), lane, p.eps);
       const long long slot = pos0 + t;
       if (split == 0 && slot >= 0 && slot < p.CAP) {  // one workgroup per (sequence, KV head) writes the cache
         bf16_t* kd = p.kc + (bh * p.CAP + slot) * MD;
         bf16_t* vd = p.vc + (bh * p.CAP + slot) * MD;
         kd[lane] = f2bf(k0);
         kd[lane + 64] = f2bf(k1);
-        vd[lane] = v0;
-        vd[lane + 64] = v1;
+        vd[lane] = kv[j][0];
+        vd[lane + 64] = kv[j][1];
       }
+      sm.knew[t][lane] = f2bf(k0);
+      sm.knew[t][lane + 64] = f2bf(k1);
+      sm.vnew[t][lane] = kv[j][0];
+      sm.vnew[t][lane + 64] = kv[j][1];
     }
-    sm.knew[t][lane] = f2bf(k0);
-    sm.knew[t][lane + 64] = f2bf(k1);
-    sm.vnew[t][lane] = v0;
-    sm.vnew[t][lane + 64] = v1;
+  }
+  // Zero rows: query rows R .. 16 MT - 1 and new-key rows T .. 31 (16-byte stores).
+  {
+    const int zq = (MT * 16 - R) * (MD / 8), zk = (MKB - T) * (MD / 8);
+    for (int z = threadIdx.x; z < zq + 2 * zk; z += 64 * WPG) {
+      bf16_t* dst;
+      if (z < zq) {
+        dst = &sm.q[R + z / (MD / 8)][8 * (z % (MD / 8))];
+      } else if (z < zq + zk) {
+        const int y = z - zq;
+        dst = &sm.knew[T + y / (MD / 8)][8 * (y % (MD / 8))];
+      } else {
+        const int y = z - zq - zk;
+        dst = &sm.vnew[T + y / (MD / 8)][8 * (y % (MD / 8))];
+      }
+      *reinterpret_cast<uint4*>(dst) = make_uint4(0, 0, 0, 0);
+    }
   }
   __syncthreads();
 
@@ -161,15 +259,6 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
       qa[mt][kt] = as_bf16x8(*reinterpret_cast<const uint4*>(&sm.q[mt * 16 + rr][32 * kt + 8 * qq]));
-
-  // ---- key partition: old keys in blocks of 32 over (split, wavefront); the new-key
-  // block goes to the last wavefront of the last split.
-  const int nblk = (nold + MKB - 1) / MKB;
-  const int per_split = (nblk + p.S - 1) / p.S;
-  const int sb0 = min(nblk, split * per_split), sb1 = min(nblk, sb0 + per_split);
-  const int per_wave = (sb1 - sb0 + WPG - 1) / WPG;
-  const int wb0 = min(sb1, sb0 + wave * per_wave), wb1 = min(sb1, wb0 + per_wave);
-  const bool takes_new = split == p.S - 1 && wave == WPG - 1;
 
   float m[MT][4], l[MT][4];
   f32x4_t o[MT][8];
@@ -183,26 +272,9 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   bf16_t* vl = &sm.u.blk.v[wave][0][0];
   bf16_t* pl = &sm.u.blk.pm[wave][0][0];
 
-  // Loads of one cached block (keys past nold re-read key 0, a valid row, and are masked).
-  mu32x4 kf[2][4], vr[8];
-  auto load_block = [&](int kb) __attribute__((always_inline)) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int key = kb + 16 * nt + rr;
-      const bf16_t* kp = kbase + (long long)(key < nold ? key : 0) * MD + 8 * qq;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) kf[nt][kt] = *reinterpret_cast<const mu32x4*>(kp + 32 * kt);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = kb + 4 * i + qq;
-      vr[i] = *reinterpret_cast<const mu32x4*>(vbase + (long long)(key < nold ? key : 0) * MD + 8 * rr);
-    }
-  };
-
   // One block: S = Q K^T, online softmax, O = O * alpha + P V. `vsrc` holds the block's V
   // rows in LDS (VROW stride); `visible(nt, row)` masks keys.
-  auto process = [&](const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
+  auto process = [&](const mu32x4 (&kf)[2][4], const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
     f32x4_t s[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -271,23 +343,39 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
     }
   };
 
-  if (wb0 < wb1) load_block(wb0 * MKB);
-  for (int blk = wb0; blk < wb1; ++blk) {
+  // One cached block: its V rows to this wavefront's LDS tile, then S / softmax / PV.
+  auto run_block = [&](const KVBlock& d, int blk) __attribute__((always_inline)) {
     const int kb = blk * MKB;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the previous block's transpose reads come first
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<mu32x4*>(vl + (4 * i + qq) * VROW + 8 * rr) = vr[i];
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<mu32x4*>(vl + (4 * i + qq) * VROW + 8 * rr) = d.v[i];
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    process(vl, [&](int nt, int row) { return kb + 16 * nt + rr < nold && row < R; });
-    if (blk + 1 < wb1) load_block((blk + 1) * MKB);
+    process(d.k, vl, [&](int nt, int row) { return kb + 16 * nt + rr < nold && row < R; });
+  };
+  if constexpr (DEPTH == 2) {
+    // Two blocks in flight: every load is unconditional (past the range: slot 0), so the
+    // compiler's wait for one block leaves the other in flight.
+    int blk = wb0;
+    for (; blk + 1 < wb1; blk += 2) {
+      run_block(blkA, blk);
+      load_block(blkA, (blk + 2) * MKB);
+      run_block(blkB, blk + 1);
+      load_block(blkB, (blk + 3) * MKB);
+    }
+    if (blk < wb1) run_block(blkA, blk);
+  } else {
+    for (int blk = wb0; blk < wb1; ++blk) {
+      run_block(blkA, blk);
+      if (blk + 1 < wb1) load_block(blkA, (blk + 1) * MKB);
+    }
   }
   if (takes_new) {  // the T new keys, from LDS; query row r (token r / 4) sees new key j iff j <= r / 4
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        kf[nt][kt] = *reinterpret_cast<const mu32x4*>(&sm.knew[16 * nt + rr][32 * kt + 8 * qq]);
-    process(&sm.vnew[0][0], [&](int nt, int row) {
+        blkA.k[nt][kt] = *reinterpret_cast<const mu32x4*>(&sm.knew[16 * nt + rr][32 * kt + 8 * qq]);
+    process(blkA.k, &sm.vnew[0][0], [&](int nt, int row) {
       const int j = 16 * nt + rr;
       return j < T && row < R && j <= row / MG;
     });
