@@ -118,10 +118,15 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
   };
 
   const int kc8 = K >> 3;
-  uint4 xv0, xv1;  // NORM: this thread's (at most two) 16-byte chunks of the rows
+  uint4 xv0, xv1, gv0, gv1;  // NORM: this thread's (at most two) 16-byte chunks of the rows + gains
   if constexpr (NORM) {
-    xv0 = xb[min((int)threadIdx.x, M * kc8 - 1)];
-    xv1 = xb[min((int)threadIdx.x + NT, M * kc8 - 1)];
+    // Requested before the weights: loads return in issue order, so anything the staging
+    // needs that is requested after the weight prefetch would wait for HBM.
+    const int c0 = min((int)threadIdx.x, M * kc8 - 1), c1 = min((int)threadIdx.x + NT, M * kc8 - 1);
+    xv0 = xb[c0];
+    xv1 = xb[c1];
+    gv0 = reinterpret_cast<const uint4*>(p.nw)[c0 % kc8];
+    gv1 = reinterpret_cast<const uint4*>(p.nw)[c1 % kc8];
   }
 #pragma unroll
   for (int s = 0; s < GV_DEPTH; ++s) issue(s);
@@ -160,12 +165,12 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
       for (int w = 0; w < WAVES; ++w) t += red[w * M + m];
       rinv[m] = 1.0f / sqrtf(t / (float)K + p.eps);
     }
-    auto stage = [&](const uint4& v, int cidx) {
+    auto stage = [&](const uint4& v, const uint4& gw, int cidx) {
       if (cidx < M * kc8) {
         const int m = cidx / kc8;
         float f[8], gn[8], o[8];
         unpack8(v, f);
-        unpack8(reinterpret_cast<const uint4*>(p.nw)[cidx - m * kc8], gn);
+        unpack8(gw, gn);
         float ri = rinv[0];
 #pragma unroll
         for (int mm = 1; mm < M; ++mm) ri = mm == m ? rinv[mm] : ri;
@@ -174,8 +179,8 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
         reinterpret_cast<uint4*>(xs)[cidx] = pack8(o);
       }
     };
-    stage(xv0, threadIdx.x);
-    stage(xv1, threadIdx.x + NT);
+    stage(xv0, gv0, threadIdx.x);
+    stage(xv1, gv1, threadIdx.x + NT);
   }
   __syncthreads();
 

@@ -214,11 +214,13 @@ MFMA_WAVES = 8
 
 def choose_mfma_splits(B: int, Nkv: int, cap: int) -> int:
     """Context splits of ``attn_decode_mfma`` for a decode shape: about 256 workgroups (one
-    per CU, each serving every query row of its KV head), at most 8, at least 128 cache slots
-    per split. Measured on MI355X at B = 1, 4, 8, 16, 32 (T = 1 and 5): the best split count
-    was within 5% of this choice at every shape."""
+    per CU, each serving every query row of its KV head), at most 8, at least 512 cache slots
+    per split (a split merge costs about what 512 keys of one workgroup's stream do).
+    Measured on MI355X: B = 1 at context 300 one split 10.0 us, two 11.2; B = 1 at 4096
+    eight splits 16 us, one 43; B = 8 at 2300 four; B = 32 at 8300 one; B = 4, T = 5 at
+    4150 eight."""
     want = max(1, 256 // max(1, B * Nkv))
-    return max(1, min(want, MFMA_MAX_SPLITS, max(1, cap // 128)))
+    return max(1, min(want, MFMA_MAX_SPLITS, max(1, cap // 512)))
 
 
 def attn_mfma_workspace(B, T, Nkv, num_splits, device) -> torch.Tensor:
