@@ -350,26 +350,8 @@ class Engine:
         else:
             assert T == 1
         gc = b["gemv_cfg"]
-        for l, w in enumerate(self.layers):
-            # M <= 2: balanced row-major GEMVs (RMSNorm statistics computed in-kernel);
-            # larger M: MFMA kernels over the tiled weights, statistics from psq.
-            if gc is not None:
-                ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
-            else:
-                ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq,
-                                 workspace=ws)
-            attn = ops.attn_decode_mfma if b["attn_mfma"] else ops.attn_decode_fused
-            attn(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T, self.k_cache[l],
-                 self.v_cache[l], self.scale, b["splits"], out=a, workspace=b["attn_ws"], waves=b["attn_waves"])
-            if gc is not None:
-                ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
-                ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, cfg=gc["gu"])
-                ops.gemv(p, w.r_down, residual=h, out=h, cfg=gc["down"])
-            else:
-                ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
-                ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p,
-                                 psq_in=psq, workspace=ws)
-                ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
+        for l in range(self.L):
+            self._layer(l, b, T)
             if hidden is not None:
                 hidden.append(h.clone())
         extract = tok is not None
@@ -381,6 +363,58 @@ class Engine:
             ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"],
                                out=b["next"] if extract else None, keys=b["keys"], psq_in=psq, extract=extract)
         return b["next"]
+
+    def _layer(self, l, b, T, trace=None):
+        """Decoder layer ``l`` of ``_step`` (``engine/engine.py:1103-1118``) on the step buffers
+        ``b``: the residual stream ``h`` (and its statistics ``psq``) is updated in place, K/V
+        are written at ``pos_buf + t``. ``trace`` (a list) receives copies of qkv, the attention
+        output, h after the O projection, the SwiGLU product and h after the down projection."""
+        M = self.B * T
+        w = self.layers[l]
+        h, qkv, a, p, psq, cfg, ws = b["h"], b["qkv"], b["a"], b["p"], b["psq"], b["cfg"], b["gemm_ws"]
+        gc = b["gemv_cfg"]
+        keep = (lambda t: trace.append(t.clone())) if trace is not None else (lambda t: None)
+        # M <= 2: balanced row-major GEMVs (RMSNorm statistics computed in-kernel);
+        # larger M: MFMA kernels over the tiled weights, statistics from psq.
+        if gc is not None:
+            ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
+        else:
+            ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq, workspace=ws)
+        keep(qkv)
+        attn = ops.attn_decode_mfma if b["attn_mfma"] else ops.attn_decode_fused
+        attn(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T, self.k_cache[l],
+             self.v_cache[l], self.scale, b["splits"], out=a, workspace=b["attn_ws"], waves=b["attn_waves"])
+        keep(a)
+        if gc is not None:
+            ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
+            keep(h)
+            ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, cfg=gc["gu"])
+            keep(p)
+            ops.gemv(p, w.r_down, residual=h, out=h, cfg=gc["down"])
+        else:
+            ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
+            keep(h)
+            ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p,
+                             psq_in=psq, workspace=ws)
+            keep(p)
+            ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
+        keep(h)
+
+    def layer_step(self, l: int, hidden: torch.Tensor, positions, T: int = 1) -> list:
+        """One decoder layer on a given residual stream ``hidden [B*T, H]`` at ``positions``
+        (the reference's single-layer case): returns the per-tensor trace of
+        ``_layer`` (qkv, attention output, h after O, SwiGLU product, h after down). Uses the
+        prepared batch and caches; eager, synchronous."""
+        assert hidden.shape == (self.B * T, self.H)
+        b = self._buffers(self.B, T)
+        trace = []
+        with torch.inference_mode():
+            self.pos_buf.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
+            b["h"].copy_(hidden.to(self.device, BF16))
+            ops.sumsq16(b["h"], out=b["psq"])
+            self._layer(l, b, T, trace=trace)
+        torch.cuda.synchronize()
+        return trace
 
     def _plain_step(self):
         """``_plain_step`` (``engine/engine.py:941-953``): step on hist[pos], write hist[pos+1], pos += 1,
