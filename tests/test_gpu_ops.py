@@ -410,6 +410,28 @@ def test_lm_head_argmax_random(qops, M):
     assert torch.equal(got[exact], logits.argmax(-1)[exact])
 
 
+@pytest.mark.parametrize("M", [8, 32])
+@pytest.mark.parametrize("V,cfgs", [(4096, [(1, 8), (2, 8), (4, 8), (8, 4), (8, 8)]), (4112, [(1, 8)])])
+def test_lm_head_launch_shapes_agree(qops, M, V, cfgs):
+    """Every LM-head launch shape (units of 1-8 n-tiles) picks the same tokens; a vocabulary of
+    257 n-tiles makes the default fall back to one n-tile per unit."""
+    K = 2560
+    g = torch.Generator().manual_seed(40 + M + V)
+    x, nw = _bf16(M, K, gen=g), _gain(K, g)
+    w = _bf16(V, K, gen=g, scale=0.02)
+    t = qops.tile_weight(w.to(DEV))
+    logits = R.linear(R.rms_norm(x, nw, EPS), w).float()
+    default = qops.lm_head_config(M, V, K)
+    assert default in cfgs
+    outs = [qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, t, cfg=c).cpu() for c in cfgs]
+    for c, o in zip(cfgs, outs):
+        assert torch.equal(o, outs[0]), f"cfg {c}"
+    top = logits.max(-1).values
+    chosen = logits.gather(-1, outs[0][:, None])[:, 0]
+    ulp = torch.tensor([2.0 ** (math.floor(math.log2(abs(float(tt)))) - 7) for tt in top])
+    assert bool(((top - chosen) <= ulp).all())
+
+
 # ---------------------------------------------------------------- step tail
 
 def _argmax_key(value: float, index: int) -> int:

@@ -351,7 +351,7 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
 
 template <int MT, int NTW, int WPG, bool NORM, int EPI>
 __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
-  constexpr int U = 4 / NTW;  // k-steps per batch (4 KB of weights); two batches in flight per wavefront
+  constexpr int U = NTW >= 4 ? 1 : 4 / NTW;  // k-steps per batch (4 KB of weights, 8 KB at NTW = 8); two in flight
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -803,6 +803,10 @@ int dispatch(const GemmParams& p, int grid, int mt, int ntw, int wpg, hipStream_
   QWEN_GEMM_W(2, 2)
   QWEN_GEMM_W(1, 4)
   QWEN_GEMM_W(2, 4)
+  if constexpr (EPI == EPI_ARGMAX) {  // LM head: wider units share each activation load over 8 n-tiles
+    QWEN_GEMM_W(1, 8)
+    QWEN_GEMM_W(2, 8)
+  }
   if constexpr (!NORM) {  // 16 wavefronts (128 VGPRs each) fit only without the norm prologue
     QWEN_GEMM_CASE(1, 1, 16)
     QWEN_GEMM_CASE(1, 2, 16)
@@ -878,9 +882,9 @@ int dispatch_rect(const GemmParams& p, int gn, int gk, int ntw, int wpg, hipStre
 int check_shape(const void* x, const void* w, int M, int N, int K, int ntw, int wpg, int ks) {
   if (!x || !w) return QWEN_ENULL;
   if (M <= 0 || M > 32 || N <= 0 || K <= 0 || K % 32 != 0) return QWEN_EARG;
-  if (ntw != 1 && ntw != 2 && ntw != 4) return QWEN_EARG;
+  if (ntw != 1 && ntw != 2 && ntw != 4 && ntw != 8) return QWEN_EARG;
   if (wpg != 4 && wpg != 8 && wpg != 16) return QWEN_EARG;
-  if (ntw == 4 && wpg == 16) return QWEN_EARG;
+  if (ntw >= 4 && wpg == 16) return QWEN_EARG;
   if (ks == 0) return (wpg == SK_WAVES && ntw <= 2) ? QWEN_OK : QWEN_EARG;  // stream-K
   if (ks < 1 || ks > 64 || ks * wpg > K / 32) return QWEN_EARG;  // every wavefront owns >= 1 k-step
   if (N % (16 * ntw) != 0) return QWEN_EARG;
