@@ -803,10 +803,8 @@ int dispatch(const GemmParams& p, int grid, int mt, int ntw, int wpg, hipStream_
   QWEN_GEMM_W(2, 2)
   QWEN_GEMM_W(1, 4)
   QWEN_GEMM_W(2, 4)
-  if constexpr (EPI == EPI_ARGMAX) {  // LM head: wider units share each activation load over 8 n-tiles
-    QWEN_GEMM_W(1, 8)
-    QWEN_GEMM_W(2, 8)
-  }
+  QWEN_GEMM_W(1, 8)  // wider units share each activation load over 8 n-tiles
+  QWEN_GEMM_W(2, 8)
   if constexpr (!NORM) {  // 16 wavefronts (128 VGPRs each) fit only without the norm prologue
     QWEN_GEMM_CASE(1, 1, 16)
     QWEN_GEMM_CASE(1, 2, 16)
@@ -897,7 +895,9 @@ int check_shape(const void* x, const void* w, int M, int N, int K, int ntw, int 
 extern "C" {
 
 long long qwen_linear_workspace_bytes(int M, int N, int ntw, int ks) {
-  if (M <= 0 || M > 32 || N <= 0 || (ntw != 1 && ntw != 2 && ntw != 4) || ks < 0 || N % (16 * ntw) != 0) return 0;
+  if (M <= 0 || M > 32 || N <= 0 || (ntw != 1 && ntw != 2 && ntw != 4 && ntw != 8) || ks < 0 ||
+      N % (16 * ntw) != 0)
+    return 0;
   if (ks == 1) return 0;
   const long long units = N / (16 * ntw);
   const long long mt = M > 16 ? 2 : 1;

@@ -320,11 +320,11 @@ def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
 # Measured launch shapes (ntw, waves, ksplit) for the Qwen3-4B projections on
 # MI355X (graph-replayed, 36 weight copies rotated), keyed by (N, K, SwiGLU
 # pair) and by M == 1, M <= 16 (one A fragment) or M <= 32 (two).
-_TUNED = {
-    (6144, 2560, False): {1: (2, 8, 1), 16: (2, 8, 1), 32: (2, 4, 1)},      # QKV
-    (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 32: (1, 4, 1)},      # O
-    (19456, 2560, True): {1: (2, 8, 1), 16: (2, 4, 1), 32: (2, 16, 256, 1)},  # gate/up + SwiGLU (32: rectangles)
-    (2560, 9728, False): {1: (1, 16, 1), 16: (1, 8, 1), 32: (2, 4, 2)},     # down
+_TUNED = {   # per M class: 1, <= 16, <= 24, <= 32 rows
+    (6144, 2560, False): {1: (2, 8, 1), 16: (2, 8, 1), 24: (2, 8, 1), 32: (2, 4, 1)},                  # QKV
+    (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 24: (1, 4, 1), 32: (1, 4, 1)},                  # O
+    (19456, 2560, True): {1: (2, 8, 1), 16: (8, 8, 1), 24: (2, 16, 256, 1), 32: (2, 16, 256, 1)},      # gate/up
+    (2560, 9728, False): {1: (1, 16, 1), 16: (2, 8, 3), 24: (2, 4, 3), 32: (2, 4, 3)},                 # down
 }
 
 
@@ -334,17 +334,18 @@ def gemm_config(M: int, N: int, K: int, silu_pair: bool = False) -> tuple:
 
     ``ksplit == 0`` selects the stream-K launch (one workgroup of 8 wavefronts
     per CU, equal weight bytes per CU). Known Qwen3-4B shapes use the measured
-    table (MI355X, graph-replayed over 36 weight copies: the rectangle launch wins
-    only for gate/up at M > 16, 30.3 vs 37.6 us at M = 32; QKV's 384 and O / down's 160
+    table (MI355X, graph-replayed over rotated weight copies: the rectangle launch wins
+    only for gate/up at M > 16, 25.5 vs 31.5 us at M = 32; QKV's 384 and O / down's 160
     n-tiles cannot be spread evenly over 256 CUs without a split-K merge that costs as
-    much as the imbalance); otherwise: 8 wavefronts per
+    much as the imbalance; down at M = 20 / 32 takes 17.3 / 18.8 us with three k-splits
+    against 19.1 / 21.0 with two); otherwise: 8 wavefronts per
     workgroup and enough workgroups (n-tile groups x k-splits) to give about
     four per CU on 256 CUs, keeping at least 4 k-steps (4 KB of weight per
     n-tile) per wavefront.
     """
     tuned = _TUNED.get((N, K, bool(silu_pair)))
     if tuned is not None:
-        return tuned[1 if M == 1 else (16 if M <= 16 else 32)]
+        return tuned[1 if M == 1 else (16 if M <= 16 else (24 if M <= 24 else 32))]
     ntw = 2 if silu_pair else 1
     waves = 8 if K // 32 >= 32 else 4
     units = N // (16 * ntw)
