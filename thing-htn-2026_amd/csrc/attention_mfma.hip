@@ -56,11 +56,17 @@ struct MfmaAttnParams {
   float scale, eps;
 };
 
-__device__ __forceinline__ void mstore_dev(float* q, float v) {
-  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Device-coherent (sc1) store / load of two adjacent fp32 values as one 64-bit access
+// (q 8-byte aligned): half the instructions of per-float accesses on the split hand-off.
+__device__ __forceinline__ void mstore2_dev(float* q, float a, float b) {
+  const unsigned long long v = ((unsigned long long)__float_as_uint(b) << 32) | __float_as_uint(a);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(q), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float mload_dev(const float* q) {
-  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void mload2_dev(const float* q, float& a, float& b) {
+  const unsigned long long v =
+      __hip_atomic_load(reinterpret_cast<const unsigned long long*>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a = __uint_as_float((unsigned)v);
+  b = __uint_as_float((unsigned)(v >> 32));
 }
 
 // One 128-wide head held as dims (c, c + 64) by lane c of a wavefront (x0, x1), with the
@@ -433,12 +439,9 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
       *reinterpret_cast<uint4*>(p.out + ((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d0) = pack8(r8);
     } else {
       float* pr = mine + (long long)row * (2 + MD);
-      if (d0 == 0) {
-        mstore_dev(pr, M);
-        mstore_dev(pr + 1, L);
-      }
+      if (d0 == 0) mstore2_dev(pr, M, L);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) mstore_dev(pr + 2 + d0 + e, acc[e]);
+      for (int e = 0; e < 8; e += 2) mstore2_dev(pr + 2 + d0 + e, acc[e], acc[e + 1]);
     }
   }
   if (p.S == 1) return;
@@ -461,10 +464,9 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
 #pragma unroll
     for (int j = 0; j < MERGE_MAX; ++j) {
       const float* ps = all + min(j, p.S - 1) * sstride + (long long)row * (2 + MD);
-      ms[j] = mload_dev(ps);
-      ls[j] = mload_dev(ps + 1);
+      mload2_dev(ps, ms[j], ls[j]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) os[j][e] = mload_dev(ps + 2 + d0 + e);
+      for (int e = 0; e < 8; e += 2) mload2_dev(ps + 2 + d0 + e, os[j][e], os[j][e + 1]);
     }
     float MM = MNEG;
 #pragma unroll
