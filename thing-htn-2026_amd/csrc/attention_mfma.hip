@@ -417,7 +417,10 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   // Thread -> (row, 8-dim chunk) items of the R x 128 result.
   constexpr int NT = 64 * WPG;
   const int items = R * (MD / 8);
-  float* mine = p.part + ((bh * p.S + split) * (MT * 16)) * (2 + MD);
+  // Split partial of (bh, split): O [16 MT][MD] fp32 (16-byte aligned rows), then (m, l) per row.
+  constexpr int PO = MT * 16 * MD, PSTRIDE = MT * 16 * (2 + MD);
+  float* mine = p.part + (bh * p.S + split) * PSTRIDE;
+  const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part + bh * p.S * PSTRIDE);
   for (int it = threadIdx.x; it < items; it += NT) {
     const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
     float M = MNEG;
@@ -438,10 +441,10 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
       for (int e = 0; e < 8; ++e) r8[e] = acc[e] / L;
       *reinterpret_cast<uint4*>(p.out + ((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d0) = pack8(r8);
     } else {
-      float* pr = mine + (long long)row * (2 + MD);
-      if (d0 == 0) mstore2_dev(pr, M, L);
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) mstore2_dev(pr + 2 + d0 + e, acc[e], acc[e + 1]);
+      if (d0 == 0) mstore2_dev(mine + PO + 2 * row, M, L);
+      const int ob = (split * PSTRIDE + row * MD + d0) * 4;
+      store16_dev(prs, ob, f32x4_t{acc[0], acc[1], acc[2], acc[3]});
+      store16_dev(prs, ob + 16, f32x4_t{acc[4], acc[5], acc[6], acc[7]});
     }
   }
   if (p.S == 1) return;
@@ -455,18 +458,22 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   }
   __syncthreads();
   if (!sm.last) return;
-  const float* all = p.part + (bh * p.S) * (MT * 16) * (2 + MD);
-  const long long sstride = (long long)(MT * 16) * (2 + MD);
+  const float* all = p.part + bh * p.S * PSTRIDE;
   for (int it = threadIdx.x; it < items; it += NT) {
     const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
     // every split's partial requested at once (S <= MERGE_MAX), merged in split order
     float ms[MERGE_MAX], ls[MERGE_MAX], os[MERGE_MAX][8];
 #pragma unroll
     for (int j = 0; j < MERGE_MAX; ++j) {
-      const float* ps = all + min(j, p.S - 1) * sstride + (long long)row * (2 + MD);
-      mload2_dev(ps, ms[j], ls[j]);
+      const int js = min(j, p.S - 1);
+      mload2_dev(all + js * PSTRIDE + PO + 2 * row, ms[j], ls[j]);
+      const int ob = (js * PSTRIDE + row * MD + d0) * 4;
+      const f32x4_t lo = load16_dev(prs, ob), hi = load16_dev(prs, ob + 16);
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) mload2_dev(ps + 2 + d0 + e, os[j][e], os[j][e + 1]);
+      for (int e = 0; e < 4; ++e) {
+        os[j][e] = lo[e];
+        os[j][e + 4] = hi[e];
+      }
     }
     float MM = MNEG;
 #pragma unroll

@@ -103,6 +103,20 @@ __device__ __forceinline__ void embed_row_tiled(const bf16_t* __restrict__ w, lo
   }
 }
 
+// Device-coherent 16-byte accesses for cross-workgroup hand-offs: raw buffer loads / stores
+// with the sc1 cache-policy bit, the same bit relaxed agent-scope atomics use (no cache flush;
+// visible to the other XCDs' workgroups once the writer's vmcnt has drained). `off` is a byte
+// offset below 2 GiB from `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7ffffffe, 0x00020000);
+}
+__device__ __forceinline__ f32x4_t load16_dev(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+__device__ __forceinline__ void store16_dev(__amdgpu_buffer_rsrc_t r, int off, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16);
+}
+
 static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
 
 // Launch-status check used by every entry point: returns the launch error.

@@ -65,24 +65,6 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Device-coherent (sc1) store / load of one fp32x4 as two relaxed agent-scope 64-bit atomic
-// accesses (global_store/load with sc1, no cache flush).
-__device__ __forceinline__ void store_dev(f32x4_t* p, const f32x4_t& v) {
-  unsigned long long* q = reinterpret_cast<unsigned long long*>(p);
-  __hip_atomic_store(q, ((unsigned long long)__float_as_uint(v[1]) << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, ((unsigned long long)__float_as_uint(v[3]) << 32) | __float_as_uint(v[2]),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ f32x4_t load_dev(const f32x4_t* p) {
-  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
-  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return f32x4_t{__uint_as_float((unsigned)a), __uint_as_float((unsigned)(a >> 32)), __uint_as_float((unsigned)b),
-                 __uint_as_float((unsigned)(b >> 32))};
-}
-
 // Monotone map of an fp32 value onto uint32 (larger float -> larger integer).
 __device__ __forceinline__ uint32_t ordered_bits(float v) {
   const uint32_t u = __float_as_uint(v);
@@ -299,12 +281,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
 template <int MT, int NTW, int EPI>
 __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int slot,
                                              int pieces, int lane) {
-  f32x4_t* base = p.part + (size_t)unit * p.piece_stride * MT * NTW * 64 + lane;
-  f32x4_t* mine = base + (size_t)slot * MT * NTW * 64;
+  f32x4_t* base = p.part + (size_t)unit * p.piece_stride * MT * NTW * 64;
+  const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(base);  // this unit's pieces: [piece][mt][nt][lane]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) store_dev(mine + (mt * NTW + nt) * 64, acc[mt][nt]);
+    for (int nt = 0; nt < NTW; ++nt) store16_dev(prs, (((slot * MT + mt) * NTW + nt) * 64 + lane) * 16, acc[mt][nt]);
   __builtin_amdgcn_s_waitcnt(0);  // partial stores complete before the arrival is counted
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   unsigned old = 0;
@@ -328,7 +310,7 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) v[jj][mt][nt] = load_dev(base + ((size_t)(j * MT + mt) * NTW + nt) * 64);
+        for (int nt = 0; nt < NTW; ++nt) v[jj][mt][nt] = load16_dev(prs, (((j * MT + mt) * NTW + nt) * 64 + lane) * 16);
     }
 #pragma unroll
     for (int jj = 0; jj < FS_BATCH; ++jj) {
