@@ -29,6 +29,8 @@ enum { GEPI_STORE = 0, GEPI_RES = 1, GEPI_SWIGLU = 2, GEPI_ARGMAX = 3 };
 
 constexpr int GV_CHUNK = 512;  // bf16 elements per row chunk: 1 KB, one wavefront load
 constexpr int GV_DEPTH = 4;    // chunks in flight per wavefront
+constexpr int GV_XC_NORM = 2;  // staged 16-byte activation chunks per thread: normed rows
+constexpr int GV_XC_PLAIN = 5; // plain rows (down projection: K = 9728 at M = 2 over 512 threads)
 
 typedef uint32_t gv_u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -105,53 +107,52 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
     }
   };
 
-  constexpr int XB = NORM ? 1 : M;  // without NORM each chunk brings its own x chunks (L2 hits)
-  uint4 buf[GV_DEPTH], bx[GV_DEPTH][XB];
+  uint4 buf[GV_DEPTH];
   auto issue = [&](int s) {
     buf[s] = gv_load_nt(wptr());
-    if constexpr (!NORM) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) bx[s][m] = left > 0 ? xb[((size_t)m * K + (size_t)ic * GV_CHUNK) / 8 + lane]
-                                                      : xb[lane];
-    }
     advance();
   };
 
+  // The activation rows are staged in LDS once per workgroup (normalised there with NORM):
+  // this thread's XC 16-byte chunks (and gains) are requested before the weights, since
+  // loads return in issue order and anything the staging needs that is requested after the
+  // weight prefetch would wait for HBM. Chunks past the rows re-read the last one (issued
+  // unconditionally, so the compiler's wait for them leaves the weights in flight).
   const int kc8 = K >> 3;
-  uint4 xv0, xv1, gv0, gv1;  // NORM: this thread's (at most two) 16-byte chunks of the rows + gains
-  if constexpr (NORM) {
-    // Requested before the weights: loads return in issue order, so anything the staging
-    // needs that is requested after the weight prefetch would wait for HBM.
-    const int c0 = min((int)threadIdx.x, M * kc8 - 1), c1 = min((int)threadIdx.x + NT, M * kc8 - 1);
-    xv0 = xb[c0];
-    xv1 = xb[c1];
-    gv0 = reinterpret_cast<const uint4*>(p.nw)[c0 % kc8];
-    gv1 = reinterpret_cast<const uint4*>(p.nw)[c1 % kc8];
+  const int nch = M * kc8;
+  constexpr int XC = NORM ? GV_XC_NORM : GV_XC_PLAIN;
+  gv_u32x4_t xv[XC], gv[NORM ? XC : 1];  // ext-vector registers (an array of uint4 would live in scratch)
+#pragma unroll
+  for (int q = 0; q < XC; ++q) {
+    const int cq = min((int)threadIdx.x + q * NT, nch - 1);
+    xv[q] = reinterpret_cast<const gv_u32x4_t*>(p.x)[cq];
+    if constexpr (NORM) gv[q] = reinterpret_cast<const gv_u32x4_t*>(p.nw)[cq % kc8];
   }
 #pragma unroll
   for (int s = 0; s < GV_DEPTH; ++s) issue(s);
+  __builtin_amdgcn_sched_barrier(0);  // the staging below stays after the weight requests
 
   for (int j = threadIdx.x; j < PR * WAVES * M; j += NT) part[j] = 0.f;
 
   if constexpr (NORM) {
-    // Stage the rows in LDS, normalised: fp32 sum of squares per row (threads in index
-    // order, then wavefronts in order), rinv, then x <- bf16(bf16(x * rinv) * gain).
+    // Normalised rows: fp32 sum of squares per row (threads in index order, then wavefronts
+    // in order), rinv, then x <- bf16(bf16(x * rinv) * gain).
     float ss[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) ss[m] = 0.f;
-    auto sumsq = [&](const uint4& v, int cidx) {
-      if (cidx < M * kc8) {
+#pragma unroll
+    for (int q = 0; q < XC; ++q) {
+      const int cidx = threadIdx.x + q * NT;
+      if (cidx < nch) {
         float f[8], t = 0.f;
-        unpack8(v, f);
+        unpack8(make_uint4(xv[q].x, xv[q].y, xv[q].z, xv[q].w), f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) t = add_rn(t, mul_rn(f[e], f[e]));
         const int m = cidx / kc8;
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) ss[mm] = add_rn(ss[mm], mm == m ? t : 0.f);
       }
-    };
-    sumsq(xv0, threadIdx.x);
-    sumsq(xv1, threadIdx.x + NT);
+    }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const float v = wave_sum(ss[m]);
@@ -165,12 +166,14 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
       for (int w = 0; w < WAVES; ++w) t += red[w * M + m];
       rinv[m] = 1.0f / sqrtf(t / (float)K + p.eps);
     }
-    auto stage = [&](const uint4& v, const uint4& gw, int cidx) {
-      if (cidx < M * kc8) {
+#pragma unroll
+    for (int q = 0; q < XC; ++q) {
+      const int cidx = threadIdx.x + q * NT;
+      if (cidx < nch) {
         const int m = cidx / kc8;
         float f[8], gn[8], o[8];
-        unpack8(v, f);
-        unpack8(gw, gn);
+        unpack8(make_uint4(xv[q].x, xv[q].y, xv[q].z, xv[q].w), f);
+        unpack8(make_uint4(gv[q].x, gv[q].y, gv[q].z, gv[q].w), gn);
         float ri = rinv[0];
 #pragma unroll
         for (int mm = 1; mm < M; ++mm) ri = mm == m ? rinv[mm] : ri;
@@ -178,9 +181,13 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
         for (int e = 0; e < 8; ++e) o[e] = mul_rn(gn[e], rbf(mul_rn(f[e], ri)));
         reinterpret_cast<uint4*>(xs)[cidx] = pack8(o);
       }
-    };
-    stage(xv0, gv0, threadIdx.x);
-    stage(xv1, gv1, threadIdx.x + NT);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < XC; ++q) {
+      const int cidx = threadIdx.x + q * NT;
+      if (cidx < nch) reinterpret_cast<gv_u32x4_t*>(xs)[cidx] = xv[q];
+    }
   }
   __syncthreads();
 
@@ -204,10 +211,8 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
       if (j + s < n) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          uint4 xv;
-          if constexpr (NORM) xv = reinterpret_cast<const uint4*>(xs + (size_t)m * K + (size_t)c * GV_CHUNK)[lane];
-          else xv = bx[s][m];
-          acc[m] = dot8(buf[s], xv, acc[m]);
+          const uint4 xc = reinterpret_cast<const uint4*>(xs + (size_t)m * K + (size_t)c * GV_CHUNK)[lane];
+          acc[m] = dot8(buf[s], xc, acc[m]);
         }
         if (++c == KC) {
           flush();
@@ -333,7 +338,8 @@ int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int 
   if (epi == GEPI_ARGMAX ? !amax : !out) return QWEN_ENULL;
   if (epi == GEPI_RES && !residual) return QWEN_ENULL;
   if (epi != GEPI_ARGMAX && ld_out < N) return QWEN_EARG;
-  if (norm_w && (long long)M * (K / 8) > 2LL * 64 * waves) return QWEN_EARG;  // <= 2 staged chunks per thread
+  const long long staged = (long long)M * (K / 8);   // 16-byte activation chunks staged per workgroup
+  if (staged > (long long)(norm_w ? GV_XC_NORM : GV_XC_PLAIN) * 64 * waves) return QWEN_EARG;
   if ((epi == GEPI_SWIGLU || epi == GEPI_ARGMAX) && !norm_w) return QWEN_EARG;  // instantiated variants
   if (epi == GEPI_RES && norm_w) return QWEN_EARG;
   const size_t lds = gemv_lds_bytes(M, N, K, grid, waves, epi);
