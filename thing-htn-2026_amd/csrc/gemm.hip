@@ -94,31 +94,53 @@ struct AOperand {
   // lanes of a row each add a contiguous quarter of them in a fixed order,
   // then the quarters are combined by a fixed butterfly, so every workgroup
   // derives bit-identical factors. The quarter is read with float4 loads that
-  // are all issued before the first add (out-of-range slots add zero).
-  __device__ __forceinline__ void stats(const GemmParams& p, int r, int q) {
+  // are all issued by stats_load (before the first weights, so that waiting
+  // for them does not wait for HBM) and added by stats_finish (out-of-range
+  // slots add zero).
+  static constexpr int MAXV = 10;  // float4 loads per lane: up to 40 partials (K <= 2560)
+  f32x4_t sv[NORM ? MT : 1][MAXV];
+
+  __device__ __forceinline__ bool stats_fast(const GemmParams& p) const {
+    const int nu = p.K >> 4;
+    return (nu & 15) == 0 && (nu >> 2) <= 4 * MAXV;
+  }
+
+  __device__ __forceinline__ void stats_load(const GemmParams& p, int r, int q) {
     if constexpr (NORM) {
+      if (!stats_fast(p)) return;
       const int nu = p.K >> 4;
       const int per = nu >> 2;
-      constexpr int MAXV = 10;  // float4 loads per lane: up to 40 partials (K <= 2560)
+      const int n4 = per >> 2;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const float* ps = p.psq_in + (size_t)(mval[mt] ? r + 16 * mt : 0) * nu;
-        float s = 0.f;
-        if ((nu & 15) == 0 && per <= 4 * MAXV) {
-          const float4* p4 = reinterpret_cast<const float4*>(ps + q * per);
-          const int n4 = per >> 2;
-          float4 v[MAXV];
+        const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(ps + q * per);
 #pragma unroll
-          for (int j = 0; j < MAXV; ++j) v[j] = p4[min(j, n4 - 1)];
+        for (int j = 0; j < MAXV; ++j) sv[mt][j] = p4[min(j, n4 - 1)];
+      }
+    }
+  }
+
+  __device__ __forceinline__ void stats_finish(const GemmParams& p, int r, int q) {
+    if constexpr (NORM) {
+      const int nu = p.K >> 4;
+      const int per = nu >> 2;
+      const bool fast = stats_fast(p);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float s = 0.f;
+        if (fast) {
+          const int n4 = per >> 2;
 #pragma unroll
           for (int j = 0; j < MAXV; ++j) {
             const float keep = j < n4 ? 1.f : 0.f;
-            s += v[j].x * keep;
-            s += v[j].y * keep;
-            s += v[j].z * keep;
-            s += v[j].w * keep;
+            s += sv[mt][j].x * keep;
+            s += sv[mt][j].y * keep;
+            s += sv[mt][j].z * keep;
+            s += sv[mt][j].w * keep;
           }
         } else {
+          const float* ps = p.psq_in + (size_t)(mval[mt] ? r + 16 * mt : 0) * nu;
           for (int u = q * per; u < (q + 1) * per; ++u) s += ps[u];
           if (nu & 3) {  // the last nu % 4 partials belong to lane q = 3
             for (int u = 4 * per; u < nu; ++u) s += q == 3 ? ps[u] : 0.f;
@@ -129,6 +151,11 @@ struct AOperand {
         rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
       }
     }
+  }
+
+  __device__ __forceinline__ void stats(const GemmParams& p, int r, int q) {
+    stats_load(p, r, q);
+    stats_finish(p, r, q);
   }
 
   // bf16x8 A fragment: raw x, or with NORM bf16(bf16(x * rinv) * gain).
@@ -150,10 +177,14 @@ struct AOperand {
 // Software-pipelined accumulation of k-steps [k0, k1) of one n-tile group:
 // a batch is U k-steps of loads (weights from HBM with non-temporal loads,
 // activations and gains from L2); the next batch is issued before the current
-// one is consumed, so two batches are in flight per wavefront. Steps past k1
-// re-read step k1-1 (a cache hit) and meet a zero A operand, so there is no
-// serial remainder loop. With `stats_after_first` the A operand's RMSNorm
-// statistics are computed once the first weights are in flight.
+// one is consumed, so two batches are in flight per wavefront. The steady-state
+// issues are unconditional (a conditional issue makes the compiler's wait at the
+// join count the batch just requested, which serialises the pipeline) and the
+// last one or two batches form a separate tail. Within a batch, weight slots
+// past k1 read a cache-resident dummy (the activation rows) and the activation
+// slots re-read step k1-1; both meet a zero A operand. With `stats_after_first`
+// the A operand's RMSNorm statistics are requested before the first weights and
+// added once those are in flight.
 template <int MT, int NTW, int U, bool NORM>
 __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NORM>& A, size_t unit, int k0, int k1,
                                            f32x4_t (&acc)[MT][NTW], int r, int q, int lane, bool stats_after_first) {
@@ -166,12 +197,13 @@ __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NOR
   struct Batch {
     uint4 bt[U][NTW], at[U][MT], gt[U];
   };
+  const uint4* dummy = reinterpret_cast<const uint4*>(p.x) + lane;
   auto issue = [&](Batch& b, int kt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kk = min(kt + u, k1 - 1);
+      const bool live = kt + u < k1;
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) b.bt[u][nt] = load_nt(wt + wrow[nt] + (size_t)kk * 64);
+      for (int nt = 0; nt < NTW; ++nt) b.bt[u][nt] = load_nt(live ? wt + wrow[nt] + (size_t)(kt + u) * 64 : dummy);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -196,14 +228,29 @@ __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NOR
     }
   };
   Batch b0, b1;
-  if (k0 < k1) issue(b0, k0);
-  if (stats_after_first) A.stats(p, r, q);
-  for (int kt = k0; kt < k1; kt += 2 * U) {
-    if (kt + U < k1) issue(b1, kt + U);
+  if (k0 >= k1) {
+    if (stats_after_first) A.stats(p, r, q);
+    return;
+  }
+  if (stats_after_first) A.stats_load(p, r, q);
+  issue(b0, k0);
+  if (stats_after_first) A.stats_finish(p, r, q);
+  // Steady state: while at least two batches follow the current one, both issues are
+  // unconditional; the last one or two batches are a separate (wavefront-uniform) tail, so
+  // no batch is requested that is not consumed.
+  int kt = k0;
+  for (; kt + 2 * U < k1; kt += 2 * U) {
+    issue(b1, kt + U);
     consume(b0, kt);
-    if (kt + U >= k1) break;
-    if (kt + 2 * U < k1) issue(b0, kt + 2 * U);
+    issue(b0, kt + 2 * U);
     consume(b1, kt + U);
+  }
+  if (kt + U < k1) {
+    issue(b1, kt + U);
+    consume(b0, kt);
+    consume(b1, kt + U);
+  } else {
+    consume(b0, kt);
   }
 }
 
@@ -335,7 +382,7 @@ template <int MT, int NTW, int WPG, bool NORM, int EPI>
 __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
   constexpr int U = NTW >= 4 ? 1 : 4 / NTW;  // k-steps per batch (4 KB of weights, 8 KB at NTW = 8); two in flight
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wavefront-uniform: scalar branches
   const int r = lane & 15, q = lane >> 4;
   const int KS = p.ks;
   const int unit = blockIdx.x / KS;
