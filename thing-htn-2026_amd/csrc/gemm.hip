@@ -185,9 +185,10 @@ struct AOperand {
 // slots re-read step k1-1; both meet a zero A operand. With `stats_after_first`
 // the A operand's RMSNorm statistics are requested before the first weights and
 // added once those are in flight.
-template <int MT, int NTW, int U, bool NORM>
+template <int MT, int NTW, int U, bool NORM, typename AfterFirst>
 __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NORM>& A, size_t unit, int k0, int k1,
-                                           f32x4_t (&acc)[MT][NTW], int r, int q, int lane, bool stats_after_first) {
+                                           f32x4_t (&acc)[MT][NTW], int r, int q, int lane, bool stats_after_first,
+                                           AfterFirst&& after_first) {
   const uint4* wt = reinterpret_cast<const uint4*>(p.w);
   const uint4* nwp = reinterpret_cast<const uint4*>(p.nw);
   const size_t KT = p.K >> 5;
@@ -230,11 +231,13 @@ __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NOR
   Batch b0, b1;
   if (k0 >= k1) {
     if (stats_after_first) A.stats(p, r, q);
+    after_first();
     return;
   }
   if (stats_after_first) A.stats_load(p, r, q);
   issue(b0, k0);
   if (stats_after_first) A.stats_finish(p, r, q);
+  after_first();
   // Steady state: while at least two batches follow the current one, both issues are
   // unconditional; the last one or two batches are a separate (wavefront-uniform) tail, so
   // no batch is requested that is not consumed.
@@ -394,6 +397,7 @@ __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
   const int k1 = min(KT, k0 + kpw);
 
   __shared__ f32x4_t red[WPG > 1 ? (WPG - 1) * MT * NTW * 64 : 1];
+  __shared__ float srinv[MT * 16];
 
   AOperand<MT, NORM> A;
   A.init(p, r, q);
@@ -402,7 +406,19 @@ __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  accumulate<MT, NTW, U, NORM>(p, A, (size_t)unit, k0, k1, acc, r, q, lane, true);
+  // RMSNorm factors: wavefront 0 derives them (the same per-wavefront code, so the same bits)
+  // while every wavefront's first weights are in flight, and shares them through LDS.
+  accumulate<MT, NTW, U, NORM>(p, A, (size_t)unit, k0, k1, acc, r, q, lane, NORM && wave == 0, [&]() {
+    if constexpr (NORM) {
+      if (wave == 0 && q == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) srinv[mt * 16 + r] = A.rinv[mt];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) A.rinv[mt] = srinv[mt * 16 + r];
+    }
+  });
 
   // Wavefront partials -> wavefront 0, summed in wavefront order.
   if constexpr (WPG > 1) {
@@ -478,7 +494,8 @@ __global__ void __launch_bounds__(64 * SK_WAVES) sk_gemm_kernel(GemmParams p) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    if (lo < hi) accumulate<MT, NTW, U, NORM>(p, A, (size_t)u, (int)(lo - u * KT), (int)(hi - u * KT), acc, r, q, lane, s == 0);
+    if (lo < hi) accumulate<MT, NTW, U, NORM>(p, A, (size_t)u, (int)(lo - u * KT), (int)(hi - u * KT), acc, r, q, lane, s == 0,
+                                              [] {});
     else if (s == 0) A.stats(p, r, q);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
