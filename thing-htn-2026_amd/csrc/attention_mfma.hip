@@ -92,7 +92,7 @@ struct MfmaSmem {
       bf16_t v[WPG][MKB][VROW];          // each wavefront's current V block
       bf16_t pm[WPG][MT * 16][MKB];      // each wavefront's P tile
     } blk;
-    float merge[WPG][MT * 16][2 + MD];   // per-wavefront (m, l, O) for the merge
+    float merge[WPG][MT * 16][MD + 4];   // per-wavefront O (16-byte aligned), then m, l for the merge
   } u;
   unsigned last;
 };
@@ -404,13 +404,16 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float* mrow = sm.u.merge[wave][mt * 16 + 4 * qq + i];
-      if (rr == 0) {
-        mrow[0] = m[mt][i];
-        mrow[1] = l[mt][i];
-      }
+      const int row = mt * 16 + 4 * qq + i;
+      if (row < R) {  // padding rows of the tile are never read back
+        float* mrow = sm.u.merge[wave][row];
+        if (rr == 0) {
+          mrow[MD] = m[mt][i];
+          mrow[MD + 1] = l[mt][i];
+        }
 #pragma unroll
-      for (int nd = 0; nd < 8; ++nd) mrow[2 + 16 * nd + rr] = o[mt][nd][i];
+        for (int nd = 0; nd < 8; ++nd) mrow[16 * nd + rr] = o[mt][nd][i];
+      }
     }
   __syncthreads();
 
@@ -423,16 +426,30 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part + bh * p.S * PSTRIDE);
   for (int it = threadIdx.x; it < items; it += NT) {
     const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
+    // every wavefront's (m, l) and 8 values requested at once (16-byte reads), then combined
+    // in wavefront order
+    f32x2_t ml[WPG];
+    f32x4_t oa[WPG], ob[WPG];
+#pragma unroll
+    for (int w = 0; w < WPG; ++w) {
+      const float* mrow = sm.u.merge[w][row];
+      ml[w] = *reinterpret_cast<const f32x2_t*>(mrow + MD);
+      oa[w] = *reinterpret_cast<const f32x4_t*>(mrow + d0);
+      ob[w] = *reinterpret_cast<const f32x4_t*>(mrow + d0 + 4);
+    }
     float M = MNEG;
 #pragma unroll
-    for (int w = 0; w < WPG; ++w) M = fmaxf(M, sm.u.merge[w][row][0]);
+    for (int w = 0; w < WPG; ++w) M = fmaxf(M, ml[w].x);
     float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < WPG; ++w) {
-      const float sc = __expf(sm.u.merge[w][row][0] - M);
-      L += sc * sm.u.merge[w][row][1];
+      const float sc = __expf(ml[w].x - M);
+      L += sc * ml[w].y;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += sc * sm.u.merge[w][row][2 + d0 + e];
+      for (int e = 0; e < 4; ++e) {
+        acc[e] += sc * oa[w][e];
+        acc[e + 4] += sc * ob[w][e];
+      }
     }
     if (p.S == 1) {
       const int t = row / MG, g = row - t * MG;
