@@ -100,7 +100,7 @@ __device__ __forceinline__ float row16_max(float v) {
 // (gain after the bf16 cast) and RoPE, bf16(bf16(y cos) + bf16(rot(y) sin)).
 __device__ __forceinline__ void mnorm_rope(float& x0, float& x1, float g0, float g1, float c0, float c1, float s0,
                                            float s1, float eps) {
-  const float ss = wave_sum(add_rn(mul_rn(x0, x0), mul_rn(x1, x1)));
+  const float ss = wave_sum_dpp(add_rn(mul_rn(x0, x0), mul_rn(x1, x1)));
   const float rinv = 1.0f / sqrtf(ss / (float)MD + eps);
   const float y0 = rbf(mul_rn(g0, rbf(mul_rn(x0, rinv))));
   const float y1 = rbf(mul_rn(g1, rbf(mul_rn(x1, rinv))));

@@ -69,6 +69,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave-wide sum without LDS round trips: each 16-lane row is summed on DPP lane permutations
+// (quad xor 1, quad xor 2, half-row mirror, row mirror: every lane of a row ends with the row
+// sum), then the four row sums are read out and added as (r0 + r1) + (r2 + r3). Fixed order
+// (deterministic); the result is uniform across the wavefront.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov_f<0x141>(v);  // row_half_mirror
+  v += dpp_mov_f<0x140>(v);  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QWEN_WAVE));

@@ -200,7 +200,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
   auto flush = [&]() {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float v = wave_sum(acc[m]);
+      const float v = wave_sum_dpp(acc[m]);
       if (lane == 0) part[((size_t)pr * WAVES + wave) * M + m] = v;
       acc[m] = 0.f;
     }
