@@ -650,7 +650,7 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
       float sacc = 0.f;
 #pragma unroll
       for (int u = 0; u < RECT_PPL; ++u) sacc += pv[i][u] * (lane + 64 * u < nu ? 1.f : 0.f);  // keeps every load used
-      rinv = 1.0f / sqrtf(wave_sum(sacc) / (float)p.K + p.eps);
+      rinv = 1.0f / sqrtf(wave_sum_dpp(sacc) / (float)p.K + p.eps);
     }
     if (m < p.M) {
 #pragma unroll

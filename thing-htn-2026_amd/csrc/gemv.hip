@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float v = wave_sum(ss[m]);
+      const float v = wave_sum_dpp(ss[m]);
       if (lane == 0) red[wave * M + m] = v;
     }
     __syncthreads();
