@@ -380,6 +380,28 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     process(d.k, vl, [&](int nt, int row) { return kb + 16 * nt + rr < nold && row < R; });
   };
+  // The T new keys, from LDS (query row r, token r / 4, sees new key j iff j <= r / 4). With
+  // one query tile and one block in flight their block runs first, in registers of its own,
+  // while the wavefront's first cached block is still on its way from HBM; otherwise (no
+  // registers to spare) it runs after the cached blocks, in theirs.
+  auto run_new = [&](mu32x4 (&kf)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        kf[nt][kt] = *reinterpret_cast<const mu32x4*>(&sm.knew[16 * nt + rr][32 * kt + 8 * qq]);
+    process(kf, &sm.vnew[0][0], [&](int nt, int row) {
+      const int j = 16 * nt + rr;
+      return j < T && row < R && j <= row / MG;
+    });
+  };
+  constexpr bool NEW_FIRST = MT == 1 && DEPTH == 1;
+  if constexpr (NEW_FIRST) {
+    if (takes_new) {
+      mu32x4 kn[2][4];
+      run_new(kn);
+    }
+  }
   if constexpr (DEPTH == 2) {
     // Two blocks in flight: every load is unconditional (past the range: slot 0), so the
     // compiler's wait for one block leaves the other in flight.
@@ -397,16 +419,8 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
       if (blk + 1 < wb1) load_block(blkA, (blk + 1) * MKB);
     }
   }
-  if (takes_new) {  // the T new keys, from LDS; query row r (token r / 4) sees new key j iff j <= r / 4
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        blkA.k[nt][kt] = *reinterpret_cast<const mu32x4*>(&sm.knew[16 * nt + rr][32 * kt + 8 * qq]);
-    process(blkA.k, &sm.vnew[0][0], [&](int nt, int row) {
-      const int j = 16 * nt + rr;
-      return j < T && row < R && j <= row / MG;
-    });
+  if constexpr (!NEW_FIRST) {
+    if (takes_new) run_new(blkA.k);
   }
 
   // ---- merge: row sums over the 16 lanes of a group, then wavefronts in order through LDS
