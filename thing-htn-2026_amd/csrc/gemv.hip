@@ -205,23 +205,34 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
       acc[m] = 0.f;
     }
   };
-  for (int j = 0; j < n; j += GV_DEPTH) {
+  auto consume = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4 xc = reinterpret_cast<const uint4*>(xs + (size_t)m * K + (size_t)c * GV_CHUNK)[lane];
+      acc[m] = dot8(buf[s], xc, acc[m]);
+    }
+    if (++c == KC) {
+      flush();
+      c = 0;
+      ++pr;
+    }
+  };
+  // Groups of GV_DEPTH chunks: every group but the last is all real and refills its slots with
+  // the next group (unconditional issues; past the range a dummy); the last group only consumes,
+  // so a wavefront's end waits for no load it does not use.
+  const int ng = (n + GV_DEPTH - 1) / GV_DEPTH;
+  int grp = 0;
+  for (; grp + 1 < ng; ++grp) {
 #pragma unroll
     for (int s = 0; s < GV_DEPTH; ++s) {
-      if (j + s < n) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const uint4 xc = reinterpret_cast<const uint4*>(xs + (size_t)m * K + (size_t)c * GV_CHUNK)[lane];
-          acc[m] = dot8(buf[s], xc, acc[m]);
-        }
-        if (++c == KC) {
-          flush();
-          c = 0;
-          ++pr;
-        }
-      }
+      consume(s);
       issue(s);
     }
+  }
+  if (ng > 0) {
+#pragma unroll
+    for (int s = 0; s < GV_DEPTH; ++s)
+      if (grp * GV_DEPTH + s < n) consume(s);
   }
   if (n > 0 && c != 0) flush();
   __syncthreads();
