@@ -28,7 +28,7 @@ namespace {
 enum { GEPI_STORE = 0, GEPI_RES = 1, GEPI_SWIGLU = 2, GEPI_ARGMAX = 3 };
 
 constexpr int GV_CHUNK = 512;  // bf16 elements per row chunk: 1 KB, one wavefront load
-constexpr int GV_DEPTH = 4;    // chunks in flight per wavefront
+constexpr int GV_DEPTH = 6;    // chunks in flight per wavefront
 constexpr int GV_XC_NORM = 2;  // staged 16-byte activation chunks per thread: normed rows
 constexpr int GV_XC_PLAIN = 5; // plain rows (down projection: K = 9728 at M = 2 over 512 threads)
 
