@@ -151,3 +151,50 @@ def test_qwen4b_shapes_greedy(qwen4b_two_layers):
         tokens = _run(eng, prompt, N, cfg["vocab_size"])
         gaps = ref.judge_gaps(prompt, tokens)
         assert float(gaps.max()) <= 0.0625, f"worst gap {float(gaps.max())}"
+
+
+# --------------------------------------------------------------- warmup certification
+# engine/engine.py:407-486: every decode-step stage and every operator of the ops table is run
+# on the production shape against its twin; the engine refuses a shape that fails.
+STAGES = {"step.norm_qkv", "step.kv_write", "step.attention", "step.o_residual", "step.norm_gate_up_swiglu",
+          "step.down_residual", "step.norm_lm_head_argmax", "rms_norm", "add_rms_norm", "silu_mul",
+          "qk_norm_rope_cache", "attn_decode"}
+
+
+@pytest.mark.parametrize("B,T,S", [(1, 1, 40), (2, 1, 9), (3, 1, 100), (8, 1, 300), (4, 5, 33), (32, 1, 64)])
+def test_certify_small(small, B, T, S):
+    eng, _ = small
+    with torch.inference_mode():
+        eng._prepare(B, S, 8)
+    verdict = eng._certify(B, T, seed=B * 10 + T)
+    assert set(verdict) == STAGES and all(verdict.values()), verdict
+    assert (B, T) in eng.certified
+
+
+@pytest.mark.parametrize("B,T,S", [(1, 1, 128), (4, 5, 4096), (32, 1, 8192)])
+def test_certify_qwen4b_shapes(qwen4b_two_layers, B, T, S):
+    """The c2, c5 and c4 step shapes and KV capacities on the real Qwen3-4B layer shapes."""
+    eng, _, _ = qwen4b_two_layers
+    with torch.inference_mode():
+        eng._prepare(B, S, 256)
+    verdict = eng._certify(B, T, seed=1)
+    assert set(verdict) == STAGES and all(verdict.values()), verdict
+
+
+def test_certify_refuses_a_mismatch(small, monkeypatch):
+    """A mistake planted in the checker (the SwiGLU twin drops the gate's SiLU; no kernel is
+    changed) fails the SwiGLU stages, raises, and leaves the shape uncertified."""
+    import engine as engine_mod
+    eng, _ = small
+    with torch.inference_mode():
+        eng._prepare(2, 12, 4)
+    eng.certified.pop((2, 1), None)
+
+    def wrong(gu):
+        i = gu.shape[-1] // 2
+        return (gu[..., :i].float() * gu[..., i:].float()).to(torch.bfloat16)
+
+    monkeypatch.setattr(engine_mod.tw, "silu_mul", wrong)
+    with pytest.raises(RuntimeError, match=r"step\.norm_gate_up_swiglu.*silu_mul"):
+        eng._certify(2, 1)
+    assert (2, 1) not in eng.certified

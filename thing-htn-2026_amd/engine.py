@@ -45,6 +45,7 @@ import torch
 import torch.nn.functional as F
 
 from qwen_hip import ops
+from qwen_hip import twins as tw
 from qwen_hip.ops import TiledWeight
 
 BF16 = torch.bfloat16
@@ -60,6 +61,9 @@ CONFIG = {
     "spec_n": 3,             # n-gram length of the draft lookup
     "spec_max_batch": 8,     # speculate only when B <= this (and B * (spec_k + 1) <= 32)
     "spec_probe": (24, 6),   # while speculation loses: plain steps between probes, spec steps per probe
+    # Run each decode-step shape's kernels against the torch twins once at warmup and refuse
+    # to decode on a mismatch (engine/engine.py:407-486; the reference falls back instead).
+    "certify": os.environ.get("QWEN_ENGINE_CERTIFY", "1") != "0",
     "log": True,
 }
 
@@ -128,6 +132,7 @@ class Engine:
         }
         self.B = self.CAP = 0
         self.graphs = {}
+        self.certified = {}
         self.step_ms = {}
         self.sdpa_mode = None
         self.decode_launches = 0   # decode steps launched since load (benchmarks read it)
@@ -265,6 +270,7 @@ class Engine:
             self.s_buf = torch.zeros((1,), dtype=torch.int64, device=dev)
             self.ntarget_buf = torch.full((1,), 1 << 40, dtype=torch.int64, device=dev)
             self.B, self.CAP, self.k_active = B, cap, k
+            self.certified = {}
             self.bufs = {}
             ring = CONFIG["pipeline_depth"] + 2
             self.pin_nxt = [torch.zeros((k + 1, B), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
@@ -272,10 +278,11 @@ class Engine:
             self.events = [torch.cuda.Event() for _ in range(ring)]
             _log(f"state B={B} CAP={cap} spec_k={k} "
                  f"kv={2 * self.L * B * self.Nkv * cap * self.D * 2 / 2**30:.2f}GiB")
-        if CONFIG["graphs"]:
-            for T in (1, k + 1) if k else (1,):
-                if T not in self.graphs:
-                    self._capture(T)
+        for T in (1, k + 1) if k else (1,):
+            if CONFIG["certify"] and (B, T) not in self.certified:
+                self._certify(B, T)
+            if CONFIG["graphs"] and T not in self.graphs:
+                self._capture(T)
 
     def _buffers(self, B, T):
         """Static activation buffers for a (B, T) step, reused by every replay."""
@@ -341,7 +348,7 @@ class Engine:
         B = self.B
         M = B * T
         b = self._buffers(B, T)
-        h, qkv, a, p, psq, cfg, ws = b["h"], b["qkv"], b["a"], b["p"], b["psq"], b["cfg"], b["gemm_ws"]
+        h, psq = b["h"], b["psq"]
         # psq holds the per-16-column sums of squares of the current residual
         # stream h: written by whoever last wrote h (embedding, O / down
         # epilogues), read by the next normed projection.
@@ -349,20 +356,24 @@ class Engine:
             ops.embed(tok.reshape(-1), self.embed, out=h, psq_out=psq)
         else:
             assert T == 1
-        gc = b["gemv_cfg"]
         for l in range(self.L):
             self._layer(l, b, T)
             if hidden is not None:
                 hidden.append(h.clone())
-        extract = tok is not None
-        if gc is not None:
-            ops.gemv(h, self.embed_rows, norm_w=self.final_norm, eps=self.eps, amax=b["keys"], cfg=gc["lm"])
+        self._lm_head(b, M, extract=tok is not None)
+        return b["next"]
+
+    def _lm_head(self, b, M, extract):
+        """Final RMSNorm + tied LM head + argmax of the step buffers ``b`` (``engine/engine.py:1119-1121``):
+        tokens into ``b["next"]`` with ``extract``, else left in the packed keys for ``decode_finish``."""
+        if b["gemv_cfg"] is not None:
+            ops.gemv(b["h"], self.embed_rows, norm_w=self.final_norm, eps=self.eps, amax=b["keys"],
+                     cfg=b["gemv_cfg"]["lm"])
             if extract:
                 ops.argmax_extract(b["keys"], M, b["next"])
         else:
-            ops.lm_head_argmax(h, self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"],
-                               out=b["next"] if extract else None, keys=b["keys"], psq_in=psq, extract=extract)
-        return b["next"]
+            ops.lm_head_argmax(b["h"], self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"],
+                               out=b["next"] if extract else None, keys=b["keys"], psq_in=b["psq"], extract=extract)
 
     def _layer(self, l, b, T, trace=None):
         """Decoder layer ``l`` of ``_step`` (``engine/engine.py:1103-1118``) on the step buffers
@@ -415,6 +426,97 @@ class Engine:
             self._layer(l, b, T, trace=trace)
         torch.cuda.synchronize()
         return trace
+
+    def _certify(self, B, T, seed=0):
+        """Warmup certification (``engine/engine.py:407-486``) of the kernels one decode step of
+        ``(B, T)`` runs, on that step's own buffers, launch configurations and KV capacity.
+
+        Layer 0 and the LM head run through ``_layer`` / ``_lm_head`` on a seeded N(0, 1) residual
+        stream, with layer 0's cache prefix filled with N(0, 1) keys and values and ragged
+        positions (every slot of it is rewritten by the prompt forward or by a decode step before
+        any step reads it). Each stage is compared with its twin (``qwen_hip.twins``) fed the
+        kernels' own output of the stage before, so a mismatch names the stage; the standalone
+        operators of the reference's ``ops`` table are checked on the same data. The bars are the
+        reference's: ``atol 1e-2, rtol 1/64``, attention ``1e-2 / 1e-2``, the V-cache copy and
+        the residual stream of ``add_rms_norm`` bit-exact, and greedy tokens within two bf16 ulps
+        of the twin's maximum logit.
+
+        Unlike the reference, a failed stage is not replaced by its twin (that would put a non-HIP
+        computation into the decode step): the engine raises ``RuntimeError`` and the shape stays
+        uncertified. Returns the verdict ``{stage: bool}`` (kept in ``self.certified[(B, T)]``).
+        """
+        M, dev, eps = B * T, self.device, self.eps
+        b = self._buffers(B, T)
+        w = self.layers[0]
+        g = torch.Generator(device=dev).manual_seed(seed)
+        gh = torch.Generator().manual_seed(seed)
+        pos = torch.randint(0, self.CAP - T, (B,), generator=gh, dtype=torch.int32)
+        pos_d = pos.to(dev)
+        lengths = pos_d + T
+        kc, vc = self.k_cache[0], self.v_cache[0]
+        Lmax = int(pos.max()) + T
+        verdict = {}
+
+        def check(name, ok):
+            verdict[name] = verdict.get(name, True) and bool(ok)
+
+        with torch.inference_mode():
+            kc[:, :, :Lmax].normal_(generator=g)
+            vc[:, :, :Lmax].normal_(generator=g)
+            h0 = torch.randn((M, self.H), generator=g, device=dev).to(BF16)
+            self.pos_buf.copy_(pos_d)
+            b["h"].copy_(h0)
+            ops.sumsq16(b["h"], out=b["psq"])
+            trace = []
+            self._layer(0, b, T, trace=trace)
+            self._lm_head(b, M, extract=True)
+            qkv_k, a_k, h1_k, p_k, h2_k = trace
+            nxt = b["next"].clone()
+            # decode-step stages, each twin fed the kernels' previous stage
+            check("step.norm_qkv", tw.close(qkv_k, tw.linear(tw.rms_norm(h0, w.ln1, eps), w.r_qkv)))
+            q_t, k_t, v_t = tw.qk_norm_rope(qkv_k, w.q_norm, w.k_norm, eps, self.cos_tab, self.sin_tab, pos_d, T,
+                                            self.Nkv)
+            bi = torch.arange(B, device=dev)[:, None].expand(B, T)
+            slots = pos_d.to(torch.int64)[:, None] + torch.arange(T, device=dev)[None, :]
+            check("step.kv_write", tw.close(kc.transpose(1, 2)[bi, slots], k_t)
+                  and torch.equal(vc.transpose(1, 2)[bi, slots], v_t))
+            a_t = tw.attention(q_t, kc, vc, lengths, self.scale)
+            check("step.attention", tw.close(a_k, a_t, atol=1e-2, rtol=1e-2))
+            o_t = tw.linear(a_k.view(M, -1), w.r_o)
+            check("step.o_residual", tw.close(h1_k, tw.add(h0, o_t)))
+            gu_t = tw.linear(tw.rms_norm(h1_k, w.ln2, eps), w.r_gu)
+            check("step.norm_gate_up_swiglu", tw.close(p_k, tw.silu_mul(gu_t)))
+            check("step.down_residual", tw.close(h2_k, tw.add(h1_k, tw.linear(p_k, w.r_down))))
+            logits = tw.linear(tw.rms_norm(h2_k, self.final_norm, eps), self.embed_rows)
+            check("step.norm_lm_head_argmax", tw.argmax_ok(nxt, logits))
+            # the reference's operator table on the same data
+            for name, op in self.ops.items():
+                if name == "rms_norm":
+                    check(name, tw.close(op(h0, w.ln1, eps), tw.rms_norm(h0, w.ln1, eps)))
+                elif name == "add_rms_norm":
+                    h_o, y_o = op(h0, o_t, w.ln2, eps)
+                    h_t = tw.add(h0, o_t)
+                    check(name, torch.equal(h_o, h_t) and tw.close(y_o, tw.rms_norm(h_t, w.ln2, eps)))
+                elif name == "silu_mul":
+                    check(name, tw.close(op(gu_t), tw.silu_mul(gu_t)))
+                elif name == "qk_norm_rope_cache":
+                    kc2, vc2 = kc.clone(), vc.clone()
+                    q_o = op(qkv_k, w.q_norm, w.k_norm, eps, self.cos_tab, self.sin_tab, pos_d, T, kc2, vc2)
+                    check(name, tw.close(q_o, q_t) and tw.close(kc2.transpose(1, 2)[bi, slots], k_t)
+                          and torch.equal(vc2.transpose(1, 2)[bi, slots], v_t))
+                    del kc2, vc2
+                elif name == "attn_decode" and T <= 16:
+                    splits = ops.choose_num_splits(B, self.Nkv, self.CAP, T)
+                    a_o = op(q_t, kc, vc, lengths.to(torch.int32), self.scale, splits)
+                    check(name, tw.close(a_o, a_t, atol=1e-2, rtol=1e-2))
+        torch.cuda.synchronize()
+        _log(f"certified on B={B} T={T}: {verdict}")
+        failed = [k for k, ok in verdict.items() if not ok]
+        if failed:
+            raise RuntimeError(f"kernel certification failed on B={B} T={T} for {failed}; "
+                               "the engine has no fallback path")
+        self.certified[(B, T)] = verdict
+        return verdict
 
     def _plain_step(self):
         """``_plain_step`` (``engine/engine.py:941-953``): step on hist[pos], write hist[pos+1], pos += 1,
