@@ -92,6 +92,17 @@ int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_n
                           void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
                           int P, float eps, float scale, int num_splits, int waves, hipStream_t stream);
 
+/* qwen_attn_decode_mfma with launch flags (flags == 0 is exactly that entry point). Bit 0
+ * (QWEN_ATTN_KV_CACHED): read the cached keys and values with ordinary, cache-allocating loads
+ * instead of non-temporal ones, for a whole KV cache small enough to stay in the Infinity
+ * Cache between steps. Other bits are rejected. Results do not depend on the flags. No
+ * reference counterpart (a load-policy choice). */
+int qwen_attn_decode_mfma_ex(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                             const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                             void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
+                             int CAP, int P, float eps, float scale, int num_splits, int waves, int flags,
+                             hipStream_t stream);
+
 /* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
  * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed
  * projections consume (psq_in below). No reference counterpart: it is the first
@@ -143,6 +154,15 @@ long long qwen_gemv_lds_bytes(int M, int N, int K, int grid, int waves, int epi)
  * (_mm / F.linear, fused_linear of engine/kernels/gemm_fused.py:136-173, lm_head + argmax). */
 int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w, float eps,
               const void* residual, int epi, unsigned long long* amax, int grid, int waves, hipStream_t stream);
+
+/* qwen_gemv with the store epilogue (epi = 0) writing weight row i's output to column
+ * row_map[i] (a permutation of [0, N), int32 on the device; row_map == NULL is qwen_gemv).
+ * No reference counterpart: it lets a caller permute a weight's rows to choose which
+ * workgroup, and so which XCD, produces each output column while the output keeps its
+ * natural layout. */
+int qwen_gemv_rowmap(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w,
+                     float eps, const void* residual, int epi, unsigned long long* amax, const int32_t* row_map,
+                     int grid, int waves, hipStream_t stream);
 
 /* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
  * token[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.

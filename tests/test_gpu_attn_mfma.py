@@ -126,3 +126,27 @@ def test_attn_decode_mfma_rejects_bad_shapes(qops, tables):
     with pytest.raises(RuntimeError, match="qwen_attn_decode_mfma failed"):   # T = 9 refused by the library too
         _lib.call("qwen_attn_decode_mfma", 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 0, B, T, NQ, NKV, D, CAP, 8192, EPS,
                   D ** -0.5, 1, 4, 0)
+
+
+@pytest.mark.parametrize("B,T,pos,CAP,splits", [(1, 1, [300], 448, 1), (2, 5, [40, 1000], 1088, 2), (1, 2, [4090], 4160, 8)])
+def test_attn_decode_mfma_kv_cached_loads_change_nothing(qops, tables, B, T, pos, CAP, splits):
+    """The cache-allocating K/V load policy gives the same output and cache writes, bit for bit."""
+    _, _, cos_d, sin_d = tables
+    qkv, kc, vc, qw, kw, p = _case(B, T, pos, CAP, 21 + B + T)
+    args = (qkv.to(DEV), qw.to(DEV), kw.to(DEV), EPS, cos_d, sin_d, p.to(DEV), T)
+    res = []
+    for cached in (False, True):
+        kd, vd = kc.to(DEV), vc.to(DEV)
+        ws = qops.attn_mfma_workspace(B, T, NKV, splits, DEV)
+        o = qops.attn_decode_mfma(*args, kd, vd, D ** -0.5, splits, workspace=ws, waves=8, kv_cached=cached)
+        torch.cuda.synchronize()
+        res.append((o.cpu(), kd.cpu(), vd.cpu()))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
+def test_attn_decode_mfma_ex_rejects_unknown_flags(qops):
+    from qwen_hip import _lib
+    with pytest.raises(RuntimeError, match="qwen_attn_decode_mfma_ex failed"):
+        _lib.call("qwen_attn_decode_mfma_ex", 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1, NQ, NKV, D, 256, 8192, EPS,
+                  D ** -0.5, 1, 8, 2, 0)

@@ -150,3 +150,34 @@ def test_gemv_rejects_bad_shapes(qops):
     w = torch.zeros(64, 512, dtype=BF16, device=DEV)
     with pytest.raises(RuntimeError, match="bad size/shape"):   # 12 wavefronts: not built
         qops.gemv(x, w, cfg=(4, 12))
+
+
+@pytest.mark.parametrize("M,N,K,grid", [(1, 6144, 2560, 256), (2, 6144, 2560, 256), (1, 300, 1536, 7)])
+def test_gemv_row_map(qops, M, N, K, grid):
+    """``qwen_gemv_rowmap``: with the weight's rows permuted and the inverse order as the row
+    map, the output lands in its natural columns and matches the oracle at the GEMV bar; the
+    two-hot case is bit-exact."""
+    g = torch.Generator().manual_seed(31 + M + N)
+    x = _bf16(M, K, gen=g)
+    w = _bf16(N, K, gen=g, scale=0.03)
+    nw = _gain(K, g)
+    perm = torch.randperm(N, generator=g)
+    want = R.linear(R.rms_norm(x, nw, EPS), w)
+    got = qops.gemv(x.to(DEV), w[perm].contiguous().to(DEV), norm_w=nw.to(DEV), eps=EPS, cfg=(grid, 8),
+                    row_map=perm.to(torch.int32).to(DEV)).cpu()
+    assert_close(got, want, 1e-2, 1 / 64, f"row map {N}x{K} M={M}")
+    xi = torch.randint(-8, 9, (M, K), generator=g).to(BF16)
+    w2 = torch.zeros(N, K, dtype=BF16)
+    cols = torch.randint(0, K, (N, 2), generator=g)
+    for n in range(N):
+        w2[n, cols[n, 0]] += 0.5
+        w2[n, cols[n, 1]] += 0.25
+    exact = (xi.double() @ w2.double().T).to(BF16)
+    got2 = qops.gemv(xi.to(DEV), w2[perm].contiguous().to(DEV), cfg=(grid, 8), row_map=perm.to(torch.int32).to(DEV))
+    assert torch.equal(got2.cpu(), exact)
+
+
+def test_gemv_row_map_only_with_store(qops):
+    from qwen_hip import _lib
+    with pytest.raises(RuntimeError, match="qwen_gemv_rowmap failed"):   # residual epilogue + map: refused
+        _lib.call("qwen_gemv_rowmap", 1, 1, 1, 1, 512, 512, 512, None, EPS, 1, 1, None, 1, 8, 8, 0)

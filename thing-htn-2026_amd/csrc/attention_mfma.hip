@@ -40,6 +40,8 @@ typedef short mv4i16 __attribute__((ext_vector_type(4)));
 typedef unsigned mu32x4 __attribute__((ext_vector_type(4)));  // 16 bytes held as a vector (stays in VGPRs)
 typedef __attribute__((address_space(3))) mv4i16 lds_mv4i16;
 
+enum { QWEN_ATTN_KV_CACHED = 1 };  // qwen_attn_decode_mfma_ex flag
+
 struct MfmaAttnParams {
   const bf16_t* qkv;      // [B*T, (Nq+2Nkv)*D]
   const bf16_t* qnw;      // [D]
@@ -54,6 +56,7 @@ struct MfmaAttnParams {
   unsigned* cnt;          // [B*Nkv] arrival counters (S > 1), zero between launches
   int T, Nkv, CAP, P, S;
   float scale, eps;
+  int kv_cached;          // cached K/V read with ordinary (cache-allocating) loads, else non-temporal
 };
 
 // Device-coherent (sc1) store / load of two adjacent fp32 values as one 64-bit access
@@ -167,16 +170,16 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int key = kb + 16 * nt + rr;
-      const bf16_t* kp = kbase + (long long)(key < kend ? key : 0) * MD + 8 * qq;
+      const mu32x4* kp = reinterpret_cast<const mu32x4*>(kbase + (long long)(key < kend ? key : 0) * MD + 8 * qq);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        d.k[nt][kt] = __builtin_nontemporal_load(reinterpret_cast<const mu32x4*>(kp + 32 * kt));
+        d.k[nt][kt] = p.kv_cached ? kp[4 * kt] : __builtin_nontemporal_load(kp + 4 * kt);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int key = kb + 4 * i + qq;
-      d.v[i] = __builtin_nontemporal_load(
-          reinterpret_cast<const mu32x4*>(vbase + (long long)(key < kend ? key : 0) * MD + 8 * rr));
+      const mu32x4* vp = reinterpret_cast<const mu32x4*>(vbase + (long long)(key < kend ? key : 0) * MD + 8 * rr);
+      d.v[i] = p.kv_cached ? *vp : __builtin_nontemporal_load(vp);
     }
   };
   // Blocks in flight per wavefront: two where the registers allow it without spilling (one
@@ -574,10 +577,12 @@ long long qwen_attn_mfma_workspace_bytes(int B, int T, int Nkv, int num_splits) 
   return mfma_counter_bytes(bh) + bh * num_splits * mfma_rows(T) * (2 + MD) * (long long)sizeof(float);
 }
 
-int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
-                          const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
-                          void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
-                          int P, float eps, float scale, int num_splits, int waves, hipStream_t stream) {
+int qwen_attn_decode_mfma_ex(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                             const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                             void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
+                             int CAP, int P, float eps, float scale, int num_splits, int waves, int flags,
+                             hipStream_t stream) {
+  if (flags & ~QWEN_ATTN_KV_CACHED) return QWEN_EARG;
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !k_cache || !v_cache || !out)
     return QWEN_ENULL;
   if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || CAP <= 0 || P <= 0) return QWEN_EARG;
@@ -601,7 +606,17 @@ int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_n
   p.part = num_splits > 1 ? (float*)((char*)workspace + mfma_counter_bytes(bh)) : nullptr;
   p.T = T; p.Nkv = Nkv; p.CAP = CAP; p.P = P; p.S = num_splits;
   p.scale = scale; p.eps = eps;
+  p.kv_cached = (flags & QWEN_ATTN_KV_CACHED) ? 1 : 0;
   return T <= 4 ? launch_mfma<1>(p, B, waves, stream) : launch_mfma<2>(p, B, waves, stream);
+}
+
+int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                          const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
+                          void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D, int CAP,
+                          int P, float eps, float scale, int num_splits, int waves, hipStream_t stream) {
+  return qwen_attn_decode_mfma_ex(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out,
+                                  workspace, workspace_bytes, B, T, Nq, Nkv, D, CAP, P, eps, scale, num_splits, waves,
+                                  0, stream);
 }
 
 }  // extern "C"

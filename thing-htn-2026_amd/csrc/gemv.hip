@@ -41,6 +41,7 @@ struct GemvParams {
   const bf16_t* res;    // [M, ld_out] residual (GEPI_RES; may alias out)
   bf16_t* out;          // [M, ld_out]
   unsigned long long* amax;  // [M] packed argmax keys (GEPI_ARGMAX), zero before the launch
+  const int32_t* rowmap;     // [N] output column of weight row i (GEPI_STORE; nullptr: column i)
   int N, K, ld_out;     // N = output columns (SwiGLU: gate/up row pairs)
   float eps;
 };
@@ -281,7 +282,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
       for (int w = 0; w < WAVES; ++w) v += part[((size_t)r * WAVES + w) * M + m];
       const size_t o = (size_t)m * p.ld_out + r0 + r;
       if constexpr (EPI == GEPI_STORE) {
-        p.out[o] = f2bf(v);
+        p.out[p.rowmap ? (size_t)m * p.ld_out + p.rowmap[r0 + r] : o] = f2bf(v);
       } else if constexpr (EPI == GEPI_RES) {
         p.out[o] = f2bf(add_rn(bf2f(p.res[o]), rbf(v)));
       } else {  // SwiGLU: gate row r, up row R + r
@@ -340,9 +341,11 @@ long long qwen_gemv_lds_bytes(int M, int N, int K, int grid, int waves, int epi)
 
 // epi: 0 store, 1 residual add (residual may alias out), 2 SwiGLU (w holds 2N rows: gate then
 // up; out has N columns), 3 argmax into amax (out unused). norm_w == nullptr: no RMSNorm prologue.
-int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w, float eps,
-              const void* residual, int epi, unsigned long long* amax, int grid, int waves, hipStream_t stream) {
+int qwen_gemv_rowmap(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w,
+                     float eps, const void* residual, int epi, unsigned long long* amax, const int32_t* row_map,
+                     int grid, int waves, hipStream_t stream) {
   if (!x || !w) return QWEN_ENULL;
+  if (row_map && epi != GEPI_STORE) return QWEN_EARG;
   if (M < 1 || M > 2 || N <= 0 || K <= 0 || K % GV_CHUNK != 0 || grid <= 0 || grid > 65536) return QWEN_EARG;
   if (waves != 8 && waves != 16) return QWEN_EARG;
   if (epi < GEPI_STORE || epi > GEPI_ARGMAX) return QWEN_EARG;
@@ -356,11 +359,16 @@ int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int 
   const size_t lds = gemv_lds_bytes(M, N, K, grid, waves, epi);
   if (lds > 160 * 1024) return QWEN_EARG;
   GemvParams p{(const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)norm_w, (const bf16_t*)residual, (bf16_t*)out,
-               amax, N, K, ld_out, eps};
+               amax, row_map, N, K, ld_out, eps};
   if (M == 1) return waves == 16 ? dispatch_gemv<1, 16>(p, norm_w != nullptr, epi, grid, lds, stream)
                                  : dispatch_gemv<1, 8>(p, norm_w != nullptr, epi, grid, lds, stream);
   return waves == 16 ? dispatch_gemv<2, 16>(p, norm_w != nullptr, epi, grid, lds, stream)
                      : dispatch_gemv<2, 8>(p, norm_w != nullptr, epi, grid, lds, stream);
+}
+
+int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w, float eps,
+              const void* residual, int epi, unsigned long long* amax, int grid, int waves, hipStream_t stream) {
+  return qwen_gemv_rowmap(x, w, out, M, N, K, ld_out, norm_w, eps, residual, epi, amax, nullptr, grid, waves, stream);
 }
 
 }  // extern "C"

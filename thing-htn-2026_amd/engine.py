@@ -64,8 +64,16 @@ CONFIG = {
     # Run each decode-step shape's kernels against the torch twins once at warmup and refuse
     # to decode on a mismatch (engine/engine.py:407-486; the reference falls back instead).
     "certify": os.environ.get("QWEN_ENGINE_CERTIFY", "1") != "0",
+    # M <= 2: order the QKV GEMV's weight rows so that each KV head's q / k / v rows are
+    # produced on the XCD that runs that head's attention workgroup.
+    "xcd_heads": os.environ.get("QWEN_ENGINE_XCD_HEADS", "1") != "0",
+    # Whole-KV-cache size up to which the decode attention reads K/V with cache-allocating
+    # loads (measured on MI355X: c2 527 -> 530 tok/s; non-temporal loads win at c4).
+    "kv_cached_max_bytes": int(os.environ.get("QWEN_ENGINE_KV_CACHED_MAX", str(128 << 20))),
     "log": True,
 }
+
+XCDS = 8   # MI355X: 8 XCDs, workgroup i of a launch runs on XCD i mod 8
 
 # Tensor ids of the counter-based random-init generator (one per HF weight).
 _PROJ_IDS = {"q_proj": 0, "k_proj": 1, "v_proj": 2, "o_proj": 3, "gate_proj": 4, "up_proj": 5, "down_proj": 6}
@@ -88,7 +96,7 @@ def random_init_scale(std: float) -> float:
 
 class _Layer:
     __slots__ = ("ln1", "w_qkv", "q_norm", "k_norm", "w_o", "ln2", "w_gu", "w_down",
-                 "r_qkv", "r_o", "r_gu", "r_down")
+                 "r_qkv", "r_o", "r_gu", "r_down", "g_qkv")
 
 
 class Engine:
@@ -133,6 +141,7 @@ class Engine:
         self.B = self.CAP = 0
         self.graphs = {}
         self.certified = {}
+        self.kv_cached = False
         self.step_ms = {}
         self.sdpa_mode = None
         self.decode_launches = 0   # decode steps launched since load (benchmarks read it)
@@ -140,12 +149,45 @@ class Engine:
         self.spec_tokens = 0       # tokens the slowest unfinished row gained from them
         self.k_active = 0          # draft tokens per verify step for the prepared batch (0: plain only)
         self._load_weights(model_path)
+        self.qkv_map = None
+        if CONFIG["xcd_heads"]:
+            order = self._qkv_xcd_order()
+            if order is not None:
+                self.qkv_map = order.to(torch.int32).to(self.device)
+                idx = order.to(self.device)
+                for w in self.layers:
+                    w.g_qkv = w.r_qkv.index_select(0, idx).contiguous()
         self._rope_max = 0
         self._ensure_rope(8192)
         torch.cuda.synchronize()
         _log(f"loaded in {time.time() - t0:.1f}s: L={self.L} H={self.H} V={self.V}")
 
     # ------------------------------------------------------------------ weights
+    def _qkv_xcd_order(self):
+        """Row order of the QKV weight for the M <= 2 GEMV in which the workgroups of one XCD
+        produce exactly one KV head group (its query heads, key and value rows), or None when
+        the shapes do not allow it.
+
+        Workgroup g of a launch runs on XCD g mod 8, the GEMV's workgroup g owns weight rows
+        [N g / G, N (g + 1) / G), and the attention's workgroup for (sequence b, KV head h)
+        is number b * Nkv + h. With Nkv = 8 and each head group exactly G / 8 workgroups of
+        rows, permuting the rows as below (and storing each output at its natural column)
+        leaves head h's q / k / v rows in the L2 of the XCD whose attention workgroup reads
+        them. Returns ``orig [N]``: permuted row p is natural row orig[p]."""
+        N = (self.Nq + 2 * self.Nkv) * self.D
+        G, _ = ops.gemv_config(1, N, self.H, ops.GEPI_STORE, self.device)
+        qd = (self.Nq // self.Nkv) * self.D
+        grp = qd + 2 * self.D
+        if self.Nkv != XCDS or N % G or G % XCDS or grp != (G // XCDS) * (N // G):
+            return None
+        rows = N // G
+        p = torch.arange(N, dtype=torch.int64)
+        g, j = p // rows, p % rows
+        h, i = g % XCDS, (g // XCDS) * rows + j
+        k0, v0 = self.Nq * self.D, (self.Nq + self.Nkv) * self.D
+        return torch.where(i < qd, h * qd + i,
+                           torch.where(i < qd + self.D, k0 + h * self.D + (i - qd), v0 + h * self.D + (i - qd - self.D)))
+
     def _load_weights(self, model_path):
         rnd = os.path.join(model_path, "random_init.json")
         if os.path.exists(rnd):
@@ -271,6 +313,10 @@ class Engine:
             self.ntarget_buf = torch.full((1,), 1 << 40, dtype=torch.int64, device=dev)
             self.B, self.CAP, self.k_active = B, cap, k
             self.certified = {}
+            # A KV cache well inside the 256 MB Infinity Cache stays there between steps when it
+            # is read with cache-allocating loads; larger ones stream with non-temporal loads.
+            kv_bytes = 2 * self.L * B * self.Nkv * cap * self.D * 2
+            self.kv_cached = kv_bytes <= CONFIG["kv_cached_max_bytes"]
             self.bufs = {}
             ring = CONFIG["pipeline_depth"] + 2
             self.pin_nxt = [torch.zeros((k + 1, B), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
@@ -388,13 +434,21 @@ class Engine:
         # M <= 2: balanced row-major GEMVs (RMSNorm statistics computed in-kernel);
         # larger M: MFMA kernels over the tiled weights, statistics from psq.
         if gc is not None:
-            ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
+            if self.qkv_map is not None:   # head h's rows produced on XCD h (see _qkv_xcd_order)
+                ops.gemv(h, w.g_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"], row_map=self.qkv_map)
+            else:
+                ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
         else:
             ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq, workspace=ws)
         keep(qkv)
-        attn = ops.attn_decode_mfma if b["attn_mfma"] else ops.attn_decode_fused
-        attn(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T, self.k_cache[l],
-             self.v_cache[l], self.scale, b["splits"], out=a, workspace=b["attn_ws"], waves=b["attn_waves"])
+        if b["attn_mfma"]:
+            ops.attn_decode_mfma(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
+                                 self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
+                                 workspace=b["attn_ws"], waves=b["attn_waves"], kv_cached=self.kv_cached)
+        else:
+            ops.attn_decode_fused(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
+                                  self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
+                                  workspace=b["attn_ws"], waves=b["attn_waves"])
         keep(a)
         if gc is not None:
             ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
@@ -566,9 +620,14 @@ class Engine:
             self._step(1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
         return [h.clone() for h in hidden]
 
+    @torch.inference_mode()
     def _capture(self, T):
         """Record one decode step into a HIP graph (``engine/engine.py:1005-1042``): the plain step
-        (T = 1) or the speculative verify step (T = k + 1)."""
+        (T = 1) or the speculative verify step (T = k + 1).
+
+        Always under inference mode: the first capture in a process creates the generator state
+        that later captures update in place, so every capture must run in the same mode (the
+        engine's own callers capture inside ``generate``)."""
         k = T - 1
         run = self._plain_step if k == 0 else (lambda: self._spec_step(k))
         pos_saved = self.pos_buf.clone()

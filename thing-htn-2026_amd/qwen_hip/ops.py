@@ -210,6 +210,7 @@ def attn_decode_fused(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions,
 MFMA_MAX_T = 8
 MFMA_MAX_SPLITS = 8
 MFMA_WAVES = 8
+ATTN_KV_CACHED = 1   # qwen_attn_decode_mfma_ex flag: cache-allocating K/V loads
 
 
 def choose_mfma_splits(B: int, Nkv: int, cap: int) -> int:
@@ -231,12 +232,13 @@ def attn_mfma_workspace(B, T, Nkv, num_splits, device) -> torch.Tensor:
 
 def attn_decode_mfma(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, T, k_cache, v_cache, scale,
                      num_splits, *, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                     waves: int = 4) -> torch.Tensor:
+                     waves: int = 4, kv_cached: bool = False) -> torch.Tensor:
     """``attn_decode_fused`` on the matrix cores (``T <= 8``, ``num_splits <= 8``).
 
     Same operator as the reference's ``qk_norm_rope_cache`` + ``attn_decode``
     (``rope.py:169-226``, ``attention.py:278-348``); one workgroup per (sequence,
-    KV head, split) serves the ``4 T`` query rows of a KV head.
+    KV head, split) serves the ``4 T`` query rows of a KV head. ``kv_cached``: read the cached
+    K/V with cache-allocating loads (for a KV cache that fits the Infinity Cache).
     """
     _gpu(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache)
     B, Nkv, CAP, D = k_cache.shape
@@ -257,10 +259,10 @@ def attn_decode_mfma(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, 
         workspace = attn_mfma_workspace(B, T, Nkv, S, qkv.device)
     o = out if out is not None else torch.empty((B, T, Nq * D), dtype=BF16, device=qkv.device)
     assert o.is_contiguous() and o.numel() == B * T * Nq * D and o.dtype == BF16
-    _lib.call("qwen_attn_decode_mfma", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+    _lib.call("qwen_attn_decode_mfma_ex", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
               cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               o.data_ptr(), workspace.data_ptr(), workspace.numel(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0],
-              float(eps), float(scale), S, int(waves), _stream())
+              float(eps), float(scale), S, int(waves), ATTN_KV_CACHED if kv_cached else 0, _stream())
     return o
 
 
@@ -512,11 +514,14 @@ def gemv_config(M: int, N: int, K: int, epi: int, device=None) -> tuple[int, int
 
 
 def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, residual=None, silu_pair: bool = False,
-         out: torch.Tensor | None = None, amax: torch.Tensor | None = None, cfg=None) -> torch.Tensor:
+         out: torch.Tensor | None = None, amax: torch.Tensor | None = None, cfg=None,
+         row_map: torch.Tensor | None = None) -> torch.Tensor:
     """``x @ w.T`` for ``x [M <= 2, K]`` over a row-major ``w [N, K]`` (``gemm_fused.py:136-173``
     semantics): optional RMSNorm prologue (``norm_w``), residual or SwiGLU epilogue
     (``silu_pair``: ``w = cat(gate, up)`` rows, output ``[M, N/2]``), or, with ``amax``, the
     first-index argmax of the bf16 logits folded into the packed int64 keys (LM head).
+    ``row_map`` (store epilogue only; int32 ``[N]``, a permutation): weight row ``i``'s output
+    goes to column ``row_map[i]``.
     """
     _gpu(x, w, norm_w, residual, out, amax)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
@@ -545,9 +550,15 @@ def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, res
             out = torch.empty((M, N), dtype=BF16, device=x.device)
         assert out.shape == (M, N) and out.is_contiguous() and out.dtype == BF16
     grid, waves = cfg if cfg is not None else gemv_config(M, N, K, epi, x.device)
-    _lib.call("qwen_gemv", x.data_ptr(), w.data_ptr(), _nullable(out) if epi != GEPI_ARGMAX else None, M, N, K,
-              N, _nullable(norm_w), float(eps), _nullable(residual), epi, _nullable(amax), int(grid), int(waves),
-              _stream())
+    if row_map is None:
+        _lib.call("qwen_gemv", x.data_ptr(), w.data_ptr(), _nullable(out) if epi != GEPI_ARGMAX else None, M, N, K,
+                  N, _nullable(norm_w), float(eps), _nullable(residual), epi, _nullable(amax), int(grid), int(waves),
+                  _stream())
+    else:
+        _gpu(row_map)
+        assert epi == GEPI_STORE and row_map.dtype == torch.int32 and row_map.numel() == N and row_map.is_contiguous()
+        _lib.call("qwen_gemv_rowmap", x.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K, N, _nullable(norm_w),
+                  float(eps), None, epi, None, row_map.data_ptr(), int(grid), int(waves), _stream())
     return amax if epi == GEPI_ARGMAX else out
 
 
