@@ -289,6 +289,10 @@ def main():
         print(json.dumps(bench_verify(eng, torch, cfg, B, S, K, W)), flush=True)
         return
     if args.profile_sample:
+        # counter calibration only: the warmup certification's KV-sized copies would sit next to
+        # the calibration copy in the counter log
+        import engine as engine_mod
+        engine_mod.CONFIG["certify"] = False
         eng._prepare(B, S, K + W + 1)
         print(json.dumps(profile_sample(eng, torch, T=SPEC_T if args.config == "c5" else 1)), flush=True)
         return

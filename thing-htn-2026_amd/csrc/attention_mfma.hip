@@ -56,7 +56,7 @@ struct MfmaAttnParams {
   unsigned* cnt;          // [B*Nkv] arrival counters (S > 1), zero between launches
   int T, Nkv, CAP, P, S;
   float scale, eps;
-  int kv_cached;          // cached K/V read with ordinary (cache-allocating) loads, else non-temporal
+  int kv_cached;          // launch the KVC = true kernel (cache-allocating K/V loads)
 };
 
 // Device-coherent (sc1) store / load of two adjacent fp32 values as one 64-bit access
@@ -126,7 +126,8 @@ struct MfmaSmem {
   unsigned last;
 };
 
-template <int MT, int WPG>
+// KVC: cached K / V read with ordinary (cache-allocating) loads instead of non-temporal ones.
+template <int MT, int WPG, bool KVC>
 __global__ void __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(1, 2)))
 attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most two wavefronts per SIMD
   __shared__ MfmaSmem<MT, WPG> sm;
@@ -172,14 +173,17 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
       const int key = kb + 16 * nt + rr;
       const mu32x4* kp = reinterpret_cast<const mu32x4*>(kbase + (long long)(key < kend ? key : 0) * MD + 8 * qq);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        d.k[nt][kt] = p.kv_cached ? kp[4 * kt] : __builtin_nontemporal_load(kp + 4 * kt);
+      for (int kt = 0; kt < 4; ++kt) {
+        if constexpr (KVC) d.k[nt][kt] = kp[4 * kt];
+        else d.k[nt][kt] = __builtin_nontemporal_load(kp + 4 * kt);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int key = kb + 4 * i + qq;
       const mu32x4* vp = reinterpret_cast<const mu32x4*>(vbase + (long long)(key < kend ? key : 0) * MD + 8 * rr);
-      d.v[i] = p.kv_cached ? *vp : __builtin_nontemporal_load(vp);
+      if constexpr (KVC) d.v[i] = *vp;
+      else d.v[i] = __builtin_nontemporal_load(vp);
     }
   };
   // Blocks in flight per wavefront: two where the registers allow it without spilling (one
@@ -560,9 +564,15 @@ int mfma_rows(int T) { return T <= 4 ? 16 : 32; }
 template <int MT>
 int launch_mfma(const MfmaAttnParams& p, int B, int waves, hipStream_t stream) {
   dim3 grid((unsigned)((long long)B * p.Nkv), p.S);
-  if (waves == 4) attn_mfma_kernel<MT, 4><<<grid, 256, 0, stream>>>(p);
-  else if (waves == 8) attn_mfma_kernel<MT, 8><<<grid, 512, 0, stream>>>(p);
-  else return QWEN_EARG;
+  if (waves == 4) {
+    if (p.kv_cached) attn_mfma_kernel<MT, 4, true><<<grid, 256, 0, stream>>>(p);
+    else attn_mfma_kernel<MT, 4, false><<<grid, 256, 0, stream>>>(p);
+  } else if (waves == 8) {
+    if (p.kv_cached) attn_mfma_kernel<MT, 8, true><<<grid, 512, 0, stream>>>(p);
+    else attn_mfma_kernel<MT, 8, false><<<grid, 512, 0, stream>>>(p);
+  } else {
+    return QWEN_EARG;
+  }
   QWEN_RETURN_LAUNCH();
 }
 

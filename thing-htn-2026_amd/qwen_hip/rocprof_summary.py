@@ -12,8 +12,8 @@ the step, and the step-to-step time.
 
 ``pmc``: average of one counter (``FETCH_SIZE`` or ``WRITE_SIZE``, KiB per
 dispatch) over the dispatches whose name contains SUBSTR, next to the same
-counter over the largest copy-like dispatches (``C`` copies of ``B`` bytes
-each way), and the scale factor ``B / (copy KiB * 1024)`` that turns the
+counter over the largest copy dispatches (``C`` copies of ``B`` bytes each way: the runtime's
+``copyBuffer`` blits, else any copy-like kernel), and the scale factor ``B / (copy KiB * 1024)`` that turns the
 counter into bytes.
 """
 
@@ -81,7 +81,10 @@ def pmc(path: str, kernel: str, copy_bytes: int, copies: int) -> str:
         names[d] = _short(r["Kernel_Name"])
         counter = r["Counter_Name"]
     target = [per[d] for d in per if kernel in names[d]]
-    copy_like = sorted(((per[d], d) for d in per if re.search(r"copy|elementwise|Copy", names[d])), reverse=True)
+    # the runtime's blit copy when present (other large elementwise kernels, such as a masked
+    # fill of a KV-sized tensor, would otherwise pass for the calibration copy)
+    copy_like = sorted(((per[d], d) for d in per if "copyBuffer" in names[d]), reverse=True) or \
+        sorted(((per[d], d) for d in per if re.search(r"copy|elementwise|Copy", names[d])), reverse=True)
     copy_vals = [v for v, _ in copy_like[:copies]]
     lines = [f"counter {counter}: {len(target)} dispatches of `{kernel}`"]
     if target:
