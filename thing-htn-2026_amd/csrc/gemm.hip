@@ -261,6 +261,21 @@ __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NOR
 template <int MT, int NTW, int EPI>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int lane) {
   const int r = lane & 15, q = lane >> 4;
+  // Residual values, all requested before any is used (rows past M re-read row 0): the
+  // residual may alias the output, so loads placed between the stores below would each wait
+  // for their own round trip.
+  float rv[EPI == EPI_RES ? MT : 1][4][EPI == EPI_RES ? NTW : 1];
+  if constexpr (EPI == EPI_RES) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 16 * mt + 4 * q + i;
+        const bf16_t* rrow = p.res + (size_t)(m < p.M ? m : 0) * p.ld_out;
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) rv[mt][i][nt] = bf2f(rrow[(unit * NTW + nt) * 16 + r]);
+      }
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -302,8 +317,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
           for (int nt = 0; nt < NTW; ++nt) {
             const long long col = (unit * NTW + nt) * 16 + r;
             if constexpr (EPI == EPI_RES) {
-              const float rv = mok ? bf2f(p.res[(size_t)m * p.ld_out + col]) : 0.f;
-              const bf16_t o = f2bf(add_rn(rv, rbf(acc[mt][nt][i])));
+              const bf16_t o = f2bf(add_rn(rv[mt][i][nt], rbf(acc[mt][nt][i])));
               if (mok) orow[col] = o;
               if (p.psq_out) {  // partial sum of squares of the new row over these 16 columns
                 const float v = bf2f(o);
