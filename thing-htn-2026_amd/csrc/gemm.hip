@@ -258,24 +258,33 @@ __device__ __forceinline__ void accumulate(const GemmParams& p, AOperand<MT, NOR
 }
 
 // Epilogue of one n-tile group (unit). Lane (q, r) holds D[16*mt + 4*q + i][16*(unit*NTW + nt) + r].
+// Residual values of one unit's output tile (EPI_RES; empty otherwise), all requested before
+// any is used (rows past M re-read row 0). The residual may alias the output, so loads placed
+// between the epilogue's stores would each wait for their own round trip.
 template <int MT, int NTW, int EPI>
-__device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int lane) {
-  const int r = lane & 15, q = lane >> 4;
-  // Residual values, all requested before any is used (rows past M re-read row 0): the
-  // residual may alias the output, so loads placed between the stores below would each wait
-  // for their own round trip.
-  float rv[EPI == EPI_RES ? MT : 1][4][EPI == EPI_RES ? NTW : 1];
-  if constexpr (EPI == EPI_RES) {
+struct ResRows {
+  float v[EPI == EPI_RES ? MT : 1][4][EPI == EPI_RES ? NTW : 1];
+  __device__ __forceinline__ void load(const GemmParams& p, long long unit, int lane) {
+    if constexpr (EPI == EPI_RES) {
+      const int r = lane & 15, q = lane >> 4;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 16 * mt + 4 * q + i;
-        const bf16_t* rrow = p.res + (size_t)(m < p.M ? m : 0) * p.ld_out;
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * mt + 4 * q + i;
+          const bf16_t* rrow = p.res + (size_t)(m < p.M ? m : 0) * p.ld_out;
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) rv[mt][i][nt] = bf2f(rrow[(unit * NTW + nt) * 16 + r]);
-      }
+          for (int nt = 0; nt < NTW; ++nt) v[mt][i][nt] = bf2f(rrow[(unit * NTW + nt) * 16 + r]);
+        }
+    }
   }
+};
+
+template <int MT, int NTW, int EPI>
+__device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int lane,
+                                         const ResRows<MT, NTW, EPI>& res) {
+  const int r = lane & 15, q = lane >> 4;
+  const auto& rv = res.v;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -338,13 +347,25 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
   }
 }
 
+template <int MT, int NTW, int EPI>
+__device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int lane) {
+  ResRows<MT, NTW, EPI> res;
+  res.load(p, unit, lane);
+  epilogue<MT, NTW, EPI>(p, acc, unit, lane, res);
+}
+
 // Cross-workgroup completion of one unit: store this workgroup's partial as
 // piece `slot` of `pieces` (device-coherent stores), count the arrival; the
 // last arriver sums the pieces in slot order (its own from registers), runs
-// the epilogue and re-arms the counter. Called by one whole wavefront.
-template <int MT, int NTW, int EPI>
+// the epilogue and re-arms the counter. Called by one whole wavefront. The residual rows
+// (EPI_RES) are requested first, so that they arrive during the store / count round trips.
+template <int MT, int NTW, int EPI, bool PRELOADED = false, int FSV = 32>
 __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)[MT][NTW], long long unit, int slot,
-                                             int pieces, int lane) {
+                                             int pieces, int lane, ResRows<MT, NTW, EPI> res = {}) {
+  // Small units request the residual before the hand-off; wide ones (where the residual, the
+  // pieces and the sums together would spill) after the pieces, in the epilogue.
+  constexpr bool EARLY = MT * NTW <= 4;
+  if constexpr (!PRELOADED && EARLY) res.load(p, unit, lane);
   f32x4_t* base = p.part + (size_t)unit * p.piece_stride * MT * NTW * 64;
   const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(base);  // this unit's pieces: [piece][mt][nt][lane]
 #pragma unroll
@@ -360,7 +381,7 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   // Pieces are requested FS_BATCH at a time (one round trip per batch rather than per
   // piece) and summed in slot order.
-  constexpr int FS_BATCH = MT * NTW >= 8 ? 1 : 8 / (MT * NTW);  // at most 32 VGPRs in flight
+  constexpr int FS_BATCH = MT * NTW * 4 >= FSV ? 1 : FSV / (MT * NTW * 4);  // at most FSV VGPRs in flight
   f32x4_t sum[MT][NTW];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -392,7 +413,8 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = sum[mt][nt];
   if (lane == 0) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  epilogue<MT, NTW, EPI>(p, acc, unit, lane);
+  if constexpr (PRELOADED || EARLY) epilogue<MT, NTW, EPI>(p, acc, unit, lane, res);
+  else epilogue<MT, NTW, EPI>(p, acc, unit, lane);
 }
 
 template <int MT, int NTW, int WPG, bool NORM, int EPI>
@@ -413,6 +435,12 @@ __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
   __shared__ f32x4_t red[WPG > 1 ? (WPG - 1) * MT * NTW * 64 : 1];
   __shared__ float srinv[MT * 16];
 
+  // Residual rows of the output tile (EPI_RES, small units): requested before anything else,
+  // unconditionally by every wavefront, so the epilogue (wavefront 0) has them without a
+  // round trip of its own.
+  constexpr bool PRE_RES = EPI == EPI_RES && MT * NTW <= 4 && WPG <= 8;  // (16 wavefronts: 128 VGPRs)
+  ResRows<MT, NTW, EPI> res;
+  if constexpr (PRE_RES) res.load(p, unit, lane);
   AOperand<MT, NORM> A;
   A.init(p, r, q);
   f32x4_t acc[MT][NTW];
@@ -450,10 +478,12 @@ __global__ void __launch_bounds__(64 * WPG) skinny_gemm_kernel(GemmParams p) {
       for (int nt = 0; nt < NTW; ++nt)
         for (int w = 1; w < WPG; ++w) acc[mt][nt] += red[(((w - 1) * MT + mt) * NTW + nt) * 64 + lane];
   }
-  if (KS > 1) {
-    finish_split<MT, NTW, EPI>(p, acc, unit, ks, KS, lane);   // split-K across workgroups
+  if constexpr (PRE_RES) {
+    if (KS > 1) finish_split<MT, NTW, EPI, true, 64>(p, acc, unit, ks, KS, lane, res);  // split-K across workgroups
+    else epilogue<MT, NTW, EPI>(p, acc, unit, lane, res);
   } else {
-    epilogue<MT, NTW, EPI>(p, acc, unit, lane);
+    if (KS > 1) finish_split<MT, NTW, EPI>(p, acc, unit, ks, KS, lane);
+    else epilogue<MT, NTW, EPI>(p, acc, unit, lane);
   }
 }
 
