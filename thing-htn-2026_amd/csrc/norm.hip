@@ -39,16 +39,28 @@ __global__ void __launch_bounds__(NORM_THREADS) rms_norm_kernel(
   uint4* yr = reinterpret_cast<uint4*>(y + row * N);
   const int nchunk = N / 8;
   // Each thread keeps at most 4 chunks (N <= 8192) in registers between passes.
+  // All chunks (and gains) are requested before any is used or any output is stored (the
+  // outputs may alias the inputs, so a load after a store would wait for its own round trip);
+  // chunks past the row re-read chunk 0 and are dropped.
   float v[4][8];
+  uint4 xv[4], rv4[4], gv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int ci = threadIdx.x + c * NORM_THREADS;
+    const int cl = ci < nchunk ? ci : 0;
+    xv[c] = xr[cl];
+    if (rr) rv4[c] = rr[cl];
+    gv[c] = wr[cl];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int ci = threadIdx.x + c * NORM_THREADS;
     if (ci < nchunk) {
-      unpack8(xr[ci], v[c]);
+      unpack8(xv[c], v[c]);
       if (rr) {
         float rv[8];
-        unpack8(rr[ci], rv);
+        unpack8(rv4[c], rv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[c][e] = rbf(add_rn(v[c][e], rv[e]));
         hr[ci] = pack8(v[c]);
@@ -64,7 +76,7 @@ __global__ void __launch_bounds__(NORM_THREADS) rms_norm_kernel(
     const int ci = threadIdx.x + c * NORM_THREADS;
     if (ci < nchunk) {
       float g[8], o[8];
-      unpack8(wr[ci], g);
+      unpack8(gv[c], g);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = mul_rn(g[e], rbf(mul_rn(v[c][e], rinv)));
       yr[ci] = pack8(o);
