@@ -154,21 +154,22 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const int nblk = (nold + MKB - 1) / MKB;
   const int per_split = (nblk + p.S - 1) / p.S;
   const int sb0 = min(nblk, split * per_split), sb1 = min(nblk, sb0 + per_split);
-  const int per_wave = (sb1 - sb0 + WPG - 1) / WPG;
-  const int wb0 = min(sb1, sb0 + wave * per_wave), wb1 = min(sb1, wb0 + per_wave);
+  // Blocks are dealt to the wavefronts in turn (wavefront w: blocks sb0 + w, sb0 + w + WPG, ..):
+  // the workgroup's K and V requests then form two contiguous streams rather than 2 * WPG.
+  constexpr int BSTEP = WPG;
+  const int wb0 = sb0 + wave, wb1 = sb1;  // this wavefront: blocks wb0, wb0 + BSTEP, .. < wb1
   const bool takes_new = split == p.S - 1 && wave == WPG - 1;
 
   // Loads of one cached block (keys past nold re-read key 0, a valid slot, and are masked).
   // A cached block's K (B operand: lane (q, r) holds key 16 nt + r, dims 32 kt + 8 q ..)
   // and V rows (lane (q, r) holds key 4 i + q, dims 8 r ..), read with non-temporal loads
   // (each cached byte is read once per step; measured on MI355X: 7.0 vs 6.2 TB/s for a
-  // plain streaming read). Keys at or past this
-  // wavefront's end (or past nold) re-read slot 0, a valid row shared by all lanes, and are
-  // masked: a prefetch past the range costs no HBM traffic.
+  // plain streaming read). Keys past nold re-read slot 0, a valid row shared by all lanes,
+  // and are masked: a prefetch past the context costs no HBM traffic.
   struct KVBlock {
     mu32x4 k[2][4], v[8];
   };
-  const int kend = min(nold, wb1 * MKB);
+  const int kend = nold;
   auto load_block = [&](KVBlock& d, int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -247,7 +248,7 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const PV kg0r = ld(p.knw[lane]), kg1r = ld(p.knw[lane + 64]);
   if constexpr (RAW) __builtin_amdgcn_sched_barrier(0);
   load_block(blkA, wb0 * MKB);  // unconditional: a wavefront without blocks re-reads valid slots
-  if constexpr (DEPTH == 2) load_block(blkB, (wb0 + 1) * MKB);
+  if constexpr (DEPTH == 2) load_block(blkB, (wb0 + BSTEP) * MKB);
   if constexpr (RAW) __builtin_amdgcn_sched_barrier(0);
   const float qg0 = fv(qg0r), qg1 = fv(qg1r), kg0 = fv(kg0r), kg1 = fv(kg1r);
 
@@ -426,17 +427,17 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
     // Two blocks in flight: every load is unconditional (past the range: slot 0), so the
     // compiler's wait for one block leaves the other in flight.
     int blk = wb0;
-    for (; blk + 1 < wb1; blk += 2) {
+    for (; blk + BSTEP < wb1; blk += 2 * BSTEP) {
       run_block(blkA, blk);
-      load_block(blkA, (blk + 2) * MKB);
-      run_block(blkB, blk + 1);
-      load_block(blkB, (blk + 3) * MKB);
+      load_block(blkA, (blk + 2 * BSTEP) * MKB);
+      run_block(blkB, blk + BSTEP);
+      load_block(blkB, (blk + 3 * BSTEP) * MKB);
     }
     if (blk < wb1) run_block(blkA, blk);
   } else {
-    for (int blk = wb0; blk < wb1; ++blk) {
+    for (int blk = wb0; blk < wb1; blk += BSTEP) {
       run_block(blkA, blk);
-      if (blk + 1 < wb1) load_block(blkA, (blk + 1) * MKB);
+      if (blk + BSTEP < wb1) load_block(blkA, (blk + BSTEP) * MKB);
     }
   }
   if constexpr (!NEW_FIRST) {
