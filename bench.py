@@ -67,7 +67,7 @@ def kv_bytes_per_token(cfg) -> int:
 
 def eng_pipeline_depth() -> int:
     from engine import CONFIG
-    return CONFIG["pipeline_depth"]
+    return CONFIG["inflight"]
 
 
 def parse():
@@ -125,35 +125,35 @@ def time_dominant_kernel(eng, torch, reps_per_layer=3, T=1):
     """
     from qwen_hip import ops
     B = eng.B
-    b = eng._buffers(B, T)
-    h, p, psq, cfg, ws = b["h"], b["p"], b["psq"], b["cfg"]["gu"], b["gemm_ws"]
+    b = eng.bufs(eng.state.groups[0], T)
+    h, p, psq, cfg, ws = b.h, b.p, b.psq, b.cfg["gu"], b.gemm_ws
     stream = torch.cuda.current_stream()
     ops.sumsq16(h, out=psq)
 
     def run(w):
-        if b["gemv"]:    # M <= 2: the balanced row-major GEMV the engine runs
-            ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, cfg=b["gemv_cfg"]["gu"])
+        if b.gemv:    # M <= 2: the balanced row-major GEMV the engine runs
+            ops.gemv(h, w.gu_rows, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, cfg=b.gemv_cfg["gu"])
         else:
-            ops.fused_linear(h, w.w_gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq,
+            ops.fused_linear(h, w.gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq,
                              workspace=ws)
 
-    for w in eng.layers[:2]:
+    for w in eng.w.layers[:2]:
         run(w)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     n = 0
     for _ in range(reps_per_layer):
-        for w in eng.layers:
+        for w in eng.w.layers:
             run(w)
             n += 1
     end.record(stream)
     end.synchronize()
     avg_s = start.elapsed_time(end) / 1e3 / n
-    w0 = eng.layers[0].w_gu
+    w0 = eng.w.layers[0].gu
     M = B * T
     bytes_launch = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
-    name = ("gemv_kernel<%d, %d, true, 2>" % (M, b["gemv_cfg"]["gu"][1]) if b["gemv"]
+    name = ("gemv_kernel<%d, %d, true, 2>" % (M, b.gemv_cfg["gu"][1]) if b.gemv
             else ops.gemm_kernel_name(M, cfg, True, ops.EPI_SWIGLU))
     return avg_s, bytes_launch, name
 
@@ -167,18 +167,18 @@ def bench_verify(eng, torch, cfg, B, S, K, W):
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
     eng.start(prompt, T * (K + W) + 8)
-    assert eng.k_active == T - 1 and T in eng.graphs, "verify graph not captured"
-    graph = eng.graphs[T][0]
+    assert eng.k_active == T - 1 and T in eng.state.graphs, "verify graph not recorded"
+    graph = eng.state.graphs[T]
     for _ in range(W):
-        graph.replay()
+        graph.launch()
     torch.cuda.synchronize()
-    pos0 = int(eng.pos_buf[0])
+    pos0 = int(eng.state.pos[0])
     t0 = time.perf_counter()
     for _ in range(K):
-        graph.replay()
+        graph.launch()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ctx_mid = (pos0 + int(eng.pos_buf[0])) / 2 + T
+    ctx_mid = (pos0 + int(eng.state.pos[0])) / 2 + T
     step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
     avg_s, k_bytes, k_name = time_dominant_kernel(eng, torch, T=T)
     achieved = k_bytes / avg_s
@@ -207,14 +207,12 @@ def cpu_baseline(eng, cfg, B, S, layers):
     import torch
     from oracle.model import CpuQwen3
 
-    def untile(t):
-        return t.data.view(t.N // 16, t.K // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(t.N, t.K).cpu()
-
     lw = []
-    for w in eng.layers[:layers]:
+    for w in eng.w.layers[:layers]:
         lw.append({"ln1": w.ln1.cpu(), "ln2": w.ln2.cpu(), "q_norm": w.q_norm.cpu(), "k_norm": w.k_norm.cpu(),
-                   "w_qkv": w.r_qkv.cpu(), "w_o": w.r_o.cpu(), "w_gu": w.r_gu.cpu(), "w_down": w.r_down.cpu()})
-    weights = {"embed": untile(eng.embed), "final_norm": eng.final_norm.cpu(), "layers": lw}
+                   "w_qkv": eng.w.natural_qkv_rows(w).cpu(), "w_o": w.o_rows.cpu(), "w_gu": w.gu_rows.cpu(),
+                   "w_down": w.down_rows.cpu()})
+    weights = {"embed": eng.w.lm_rows.cpu(), "final_norm": eng.w.final_norm.cpu(), "layers": lw}
     ref = CpuQwen3(dict(cfg, num_hidden_layers=layers), weights)
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -293,7 +291,7 @@ def main():
         # the calibration copy in the counter log
         import engine as engine_mod
         engine_mod.CONFIG["certify"] = False
-        eng._prepare(B, S, K + W + 1)
+        eng.prepare(B, S, K + W + 1)
         print(json.dumps(profile_sample(eng, torch, T=SPEC_T if args.config == "c5" else 1)), flush=True)
         return
     g = torch.Generator().manual_seed(1)
@@ -306,13 +304,13 @@ def main():
     for _ in range(W):
         next(gen)
     torch.cuda.synchronize()
-    l0 = eng.decode_launches
+    l0 = eng.counters["decode"]
     t0 = time.perf_counter()
     for _ in gen:
         pass
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    steps = eng.decode_launches - l0
+    steps = eng.counters["decode"] - l0
     if steps <= 0:
         sys.exit(f"bench.py: no decode step was launched inside the timed window (--steps {K} is within the "
                  f"engine's {eng_pipeline_depth()} steps of pipelining); use more steps")

@@ -211,6 +211,25 @@ int qwen_spec_accept(const int64_t* nxt, const int64_t* tok, int64_t* hist, int3
                      const int64_t* ntarget, int B, int cap, int T, int64_t* out_t, int64_t* adv_out,
                      const void* w_tiled, void* h, float* psq, long long V, int K, hipStream_t stream);
 
+/* Prompt-forward projection: out = x @ W^T for any M over a tiled weight, fp32 accumulation,
+ * epilogue epi = 0 store (bf16(acc)), 1 residual add (out = bf16(residual + bf16(acc));
+ * residual may alias out), 2 SwiGLU (pair-interleaved gate|up weight of N = 2I rows; out has
+ * I columns: bf16(bf16(silu(bf16(g))) * bf16(u))). x: [M, K] row-major with M * K < 2^31;
+ * N % 128 == 0, K % 64 == 0; out / residual: [M, ld_out], ld_out % 8 == 0.
+ * Replaces the prompt forward's projections, engine/engine.py:1191-1221 (_mm / cuBLAS on
+ * B*S rows) with the fused epilogues of engine/kernels/gemm_fused.py:136-173. */
+int qwen_gemm(const void* x, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* residual,
+              int epi, hipStream_t stream);
+
+/* Causal attention of a prompt chunk: q [B, T, Nq, D] (normed + rotated queries of positions
+ * p0 .. p0 + T - 1 of every sequence), caches [B, Nkv, CAP, D] already holding those
+ * positions' keys / values; query t sees slots [0, p0 + t]. out [B, T, Nq * D] bf16.
+ * Nq == 4 * Nkv, D == 128, p0 + T <= CAP. Rounding points of the decode attention
+ * (fp32 scores * scale, bf16 probabilities for PV, fp32 sums, one final rounding).
+ * Replaces engine/engine.py:1123-1179 (_prefill_attention: SDPA flash, causal, GQA). */
+int qwen_attn_prefill(const void* q, const void* k_cache, const void* v_cache, void* out, int B, int T, int Nq,
+                      int Nkv, int D, int CAP, int p0, float scale, hipStream_t stream);
+
 /* Row-major [N, K] bf16 -> tiled layout (pair = 1: gate|up interleave, tile 2p = rows
  * 16p.., tile 2p+1 = rows N/2 + 16p..). Replaces the weight fusion / layout step of
  * engine/engine.py:209-227 (the reference keeps row-major; this build re-lays for MFMA). */

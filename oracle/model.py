@@ -48,6 +48,8 @@ class CpuQwen3:
         self.w = weights
         self.B = self.CAP = 0
         self.cos_tab = self.sin_tab = None
+        # the LM head: tied to the embedding unless the weights hold their own (engine/engine.py:225-226)
+        self.lm_head = weights.get("lm_head", weights["embed"])
 
     # ------------------------------------------------------------- weights
     @classmethod
@@ -130,7 +132,7 @@ class CpuQwen3:
         for l in range(self.L):
             h, d = self.layer(l, h, d, pos, T, B, hidden)
         _, n = R.add_rms_norm(h, d, self.w["final_norm"], self.eps)
-        logits = R.linear(n, self.w["embed"])
+        logits = R.linear(n, self.lm_head)
         nxt = R.argmax_lowest(logits)
         return (nxt, logits) if return_logits else nxt
 
@@ -156,8 +158,13 @@ class CpuQwen3:
         self.pos += adv.to(torch.int32)
         return nxt, adv
 
-    def prefill(self, ids: torch.Tensor, hidden=None, return_logits=False):
-        """``_prefill_slice`` for the whole batch (``engine/engine.py:1191-1221``)."""
+    def prefill(self, ids: torch.Tensor, hidden=None, return_logits=False, positions=None):
+        """``_prefill_slice`` for the whole batch (``engine/engine.py:1191-1221``).
+
+        Returns the greedy token after the last prompt position (and its bf16 logits with
+        ``return_logits``). ``positions`` (a list of prompt positions) instead returns the bf16
+        logits ``[B, len(positions), V]`` predicting the token after each of them.
+        """
         B, S = ids.shape
         pos = torch.zeros((B,), dtype=torch.int32)
         h = self.w["embed"][ids.reshape(-1)]
@@ -178,11 +185,24 @@ class CpuQwen3:
             d = R.linear(R.silu_mul(R.linear(n, w["w_gu"])), w["w_down"])
             if hidden is not None:
                 hidden.append(R.add_rms_norm(h, d, w["ln1"], self.eps)[0])
+        if positions is not None:
+            rows = (torch.arange(B)[:, None] * S + torch.as_tensor(positions)[None, :]).reshape(-1)
+            _, n = R.add_rms_norm(h[rows], d[rows], self.w["final_norm"], self.eps)
+            return R.linear(n, self.lm_head).view(B, len(positions), -1)
         last = torch.arange(B) * S + (S - 1)
         _, n = R.add_rms_norm(h[last], d[last], self.w["final_norm"], self.eps)
-        logits = R.linear(n, self.w["embed"])
+        logits = R.linear(n, self.lm_head)
         nxt = R.argmax_lowest(logits)
         return (nxt, logits) if return_logits else nxt
+
+    def replay_logits(self, prompt, tokens):
+        """bf16 logits ``[B, N, V]`` predicting each emitted token from its own prefix, from ONE
+        teacher-forced forward over prompt + emitted tokens, as the reference's judge does
+        (``tests/local_check.py:254-272``: logits at positions ``S - 1 .. S + N - 2``)."""
+        B, S, N = len(prompt), len(prompt[0]), len(tokens[0])
+        ids = torch.tensor([list(prompt[b]) + list(tokens[b][:-1]) for b in range(B)], dtype=torch.int64)
+        self.prepare(B, ((S + N + 63) // 64) * 64)
+        return self.prefill(ids, positions=list(range(S - 1, S + N - 1)))
 
     def teacher_forced_logits(self, prompt, tokens):
         """bf16 logits ``[B, N, V]`` predicting each emitted token from its own prefix.

@@ -1,10 +1,10 @@
 """GPU tests of the drop-in Engine: protocol, state handling and greedy parity with the CPU oracle.
 
-The parity rule is the reference judge's (``tests/local_check.py:254-271``),
-teacher-forced on the engine's own tokens, with the margin tightened from 2.0
-logits to one bf16 ulp at the logit magnitude (a token may differ from the
-oracle's argmax only inside a bf16 near-tie). Protocol and state cases mirror
-``tests/local_check.py:47-54`` and ``:197-230``.
+Greedy parity is the north-star rule, checked like the reference's judge (one teacher-forced
+forward over prompt + emitted tokens, ``tests/local_check.py:254-337``): every emitted token
+must be the oracle's argmax except at steps where the oracle's top-2 logit gap is below 1e-2
+(``helpers.assert_greedy_parity``). Protocol and state cases mirror ``tests/local_check.py:47-54``
+and ``:197-230``; the launch count mirrors ``tests/launch_count.py:57-65``.
 """
 
 import itertools
@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from __graft_entry__ import write_random_model
+from helpers import assert_greedy_parity
 from oracle.model import QWEN3_4B, CpuQwen3
 
 pytestmark = pytest.mark.gpu
@@ -28,6 +29,10 @@ STD = 0.05
 def _prompt(B, S, V, seed):
     g = torch.Generator().manual_seed(seed * 1_000_003 + 7_919 + 1)
     return torch.randint(0, V, (B, S), generator=g).tolist()
+
+
+def _periodic(period, S):
+    return (period * (S // len(period) + 1))[:S]
 
 
 def _run(engine, prompt, N, V):
@@ -47,23 +52,32 @@ def small(tmp_path_factory):
     return Engine(path), CpuQwen3.random_init(SMALL, seed=0, std=STD)
 
 
-@pytest.mark.parametrize("B,S,N", [(1, 5, 4), (2, 17, 6), (3, 64, 4), (1, 130, 9), (8, 40, 5)])
+@pytest.mark.parametrize("B,S,N", [(1, 5, 4), (2, 17, 6), (3, 64, 4), (1, 130, 9), (8, 40, 5), (32, 9, 4)])
 def test_generate_matches_oracle(small, B, S, N):
     eng, ref = small
     prompt = _prompt(B, S, SMALL["vocab_size"], B * 100 + S)
     tokens = _run(eng, prompt, N, SMALL["vocab_size"])
-    gaps = ref.judge_gaps(prompt, tokens)
-    assert float(gaps.max()) <= 0.0625, f"worst gap {float(gaps.max())}"
+    assert_greedy_parity(ref, prompt, tokens, f"small B={B} S={S} N={N}")
+
+
+def test_more_than_32_sequences(small):
+    """B > 32 decodes as row groups of at most 32 sequences inside one step."""
+    eng, ref = small
+    B, S, N = 40, 12, 5
+    prompt = _prompt(B, S, SMALL["vocab_size"], 4040)
+    tokens = _run(eng, prompt, N, SMALL["vocab_size"])
+    assert len(eng.state.groups) == 2 and [g.n for g in eng.state.groups] == [32, 8]
+    assert_greedy_parity(ref, prompt, tokens, "small B=40")
 
 
 def test_state_leak_and_batch_change(small):
     eng, ref = small
     V = SMALL["vocab_size"]
     for i, (name, B, S, N) in enumerate([("leak-1", 2, 17, 6), ("leak-2", 2, 17, 6), ("bchange-3", 3, 17, 6),
-                                         ("bchange-1", 1, 17, 6)]):
+                                         ("bchange-1", 1, 17, 6), ("longer", 1, 300, 40)]):
         prompt = _prompt(B, S, V, 500 + i)
         tokens = _run(eng, prompt, N, V)
-        assert float(ref.judge_gaps(prompt, tokens).max()) <= 0.0625, name
+        assert_greedy_parity(ref, prompt, tokens, name)
 
 
 def test_zero_and_one_tokens(small):
@@ -73,31 +87,34 @@ def test_zero_and_one_tokens(small):
     assert len(out) == 1 and len(out[0]) == 1
 
 
-def test_rejects_bad_token_ids(small):
+def test_rejects_bad_input(small):
     eng, _ = small
     with pytest.raises(ValueError):
         list(eng.generate([[1, SMALL["vocab_size"]]], 2))
+    with pytest.raises(ValueError):
+        list(eng.generate([[1, 2], [3]], 2))
 
 
-def test_exactly_n_minus_one_decode_steps(small, monkeypatch):
-    """``tests/launch_count.py:57-65``: plain decoding launches exactly N-1 steps."""
+@pytest.mark.parametrize("graphs", [False, True])
+def test_exactly_n_minus_one_decode_steps(small, monkeypatch, graphs):
+    """``tests/launch_count.py:57-65``: plain decoding launches exactly N - 1 steps."""
     eng, _ = small
     import engine as engine_mod
-    monkeypatch.setitem(engine_mod.CONFIG, "graphs", False)
-    eng.graphs = {}       # the next generate() with graphs on captures afresh
+    monkeypatch.setitem(engine_mod.CONFIG, "graphs", graphs)
     calls = {"n": 0}
-    real = eng._plain_step
+    real = eng._plain
 
     def counted():
         calls["n"] += 1
         return real()
 
-    monkeypatch.setattr(eng, "_plain_step", counted)
+    monkeypatch.setattr(eng, "_plain", counted)
+    before = eng.counters["decode"]
     _run(eng, _prompt(2, 9, SMALL["vocab_size"], 3), 7, SMALL["vocab_size"])
-    assert calls["n"] == 6
+    assert calls["n"] == 6 and eng.counters["decode"] - before == 6
 
 
-def test_verify_step_matches_plain_steps(small):
+def test_verify_step_matches_oracle(small):
     """A T=5 verify forward (speculative-verify shape) gives each position's greedy token."""
     eng, ref = small
     B, S, T = 4, 33, 5
@@ -113,8 +130,9 @@ def test_verify_step_matches_plain_steps(small):
     pos = torch.full((B,), S, dtype=torch.int32)
     _, logits = ref.step(tok, pos, T, return_logits=True)
     logits = logits.float().view(B, T, -1)
-    gap = logits.amax(-1) - logits.gather(-1, got[..., None])[..., 0]
-    assert float(gap.max()) <= 0.0625
+    top2 = logits.topk(2, dim=-1).values
+    ok = (logits.argmax(-1) == got) | ((top2[..., 0] - top2[..., 1]) < 1e-2)
+    assert bool(ok.all()), (got, logits.argmax(-1))
 
 
 @pytest.fixture(scope="module")
@@ -144,13 +162,42 @@ def test_qwen4b_shapes_hidden_states(qwen4b_two_layers):
         assert rel <= 2e-2, f"layer {l}: relative error {rel}"
 
 
-def test_qwen4b_shapes_greedy(qwen4b_two_layers):
+@pytest.mark.parametrize("B,S,N", [(1, 40, 6), (4, 17, 4), (8, 300, 5)])
+def test_qwen4b_shapes_greedy(qwen4b_two_layers, B, S, N):
+    """B = 8 runs c3's M = 8 launch shapes (skinny MFMA GEMMs, the 4-split attention)."""
     eng, ref, cfg = qwen4b_two_layers
-    for B, S, N in [(1, 40, 6), (4, 17, 4)]:
-        prompt = _prompt(B, S, cfg["vocab_size"], B + S)
-        tokens = _run(eng, prompt, N, cfg["vocab_size"])
-        gaps = ref.judge_gaps(prompt, tokens)
-        assert float(gaps.max()) <= 0.0625, f"worst gap {float(gaps.max())}"
+    prompt = _prompt(B, S, cfg["vocab_size"], B + S)
+    tokens = _run(eng, prompt, N, cfg["vocab_size"])
+    assert_greedy_parity(ref, prompt, tokens, f"qwen4b-2L B={B} S={S} N={N}")
+
+
+def test_qwen4b_shapes_c3_capacity(qwen4b_two_layers):
+    """c3's batch state: B = 8 with a 2048-token prompt (capacity above 2.5k slots)."""
+    eng, ref, cfg = qwen4b_two_layers
+    B, S, N = 8, 2048, 4
+    prompt = _prompt(B, S, cfg["vocab_size"], 2048)
+    tokens = _run(eng, prompt, N, cfg["vocab_size"])
+    assert eng.CAP >= S + N and eng.state.bufs[(0, 1)].splits == 4
+    assert_greedy_parity(ref, prompt, tokens, "qwen4b-2L c3 shape")
+
+
+def test_qwen4b_speculation_periodic(qwen4b_two_layers, monkeypatch):
+    """c5's verify path on Qwen3-4B shapes with drafts that get accepted: periodic prompts
+    (``tests/spec_check.py:26-85``), speculation on every step, greedy parity on every token."""
+    import engine as engine_mod
+    eng, ref, cfg = qwen4b_two_layers
+    monkeypatch.setitem(engine_mod.CONFIG, "spec_k", 4)
+    monkeypatch.setitem(engine_mod.CONFIG, "spec_policy", "always")
+    prompt = [_periodic([11, 220, 3, 500, 77, 9, 42], 96), _periodic([5, 6, 7, 8, 9], 96),
+              _periodic([1000, 2000, 3000], 96), _periodic([42] * 3 + [43], 96)]
+    before = dict(eng.counters)
+    tokens = _run(eng, prompt, 24, cfg["vocab_size"])
+    assert eng.k_active == 4
+    verify = eng.counters["verify"] - before["verify"]
+    gained = eng.counters["verify_gain"] - before["verify_gain"]
+    print(f"qwen4b speculation: {verify} verify steps, {gained} tokens for the slowest row")
+    assert verify > 0
+    assert_greedy_parity(ref, prompt, tokens, "qwen4b-2L periodic speculation")
 
 
 # --------------------------------------------------------------- warmup certification
@@ -165,19 +212,19 @@ STAGES = {"step.norm_qkv", "step.kv_write", "step.attention", "step.o_residual",
 def test_certify_small(small, B, T, S):
     eng, _ = small
     with torch.inference_mode():
-        eng._prepare(B, S, 8)
-    verdict = eng._certify(B, T, seed=B * 10 + T)
+        eng.prepare(B, S, 8)
+    verdict = eng.certify(eng.state.groups[0], T, seed=B * 10 + T)
     assert set(verdict) == STAGES and all(verdict.values()), verdict
-    assert (B, T) in eng.certified
+    assert (B, T) in eng.state.certified
 
 
-@pytest.mark.parametrize("B,T,S", [(1, 1, 128), (4, 5, 4096), (32, 1, 8192)])
+@pytest.mark.parametrize("B,T,S", [(1, 1, 128), (8, 1, 2048), (4, 5, 4096), (32, 1, 8192)])
 def test_certify_qwen4b_shapes(qwen4b_two_layers, B, T, S):
-    """The c2, c5 and c4 step shapes and KV capacities on the real Qwen3-4B layer shapes."""
+    """The c2, c3, c5 and c4 step shapes and KV capacities on the real Qwen3-4B layer shapes."""
     eng, _, _ = qwen4b_two_layers
     with torch.inference_mode():
-        eng._prepare(B, S, 256)
-    verdict = eng._certify(B, T, seed=1)
+        eng.prepare(B, S, 256)
+    verdict = eng.certify(eng.state.groups[0], T, seed=1)
     assert set(verdict) == STAGES and all(verdict.values()), verdict
 
 
@@ -187,8 +234,8 @@ def test_certify_refuses_a_mismatch(small, monkeypatch):
     import engine as engine_mod
     eng, _ = small
     with torch.inference_mode():
-        eng._prepare(2, 12, 4)
-    eng.certified.pop((2, 1), None)
+        eng.prepare(2, 12, 4)
+    eng.state.certified.pop((2, 1), None)
 
     def wrong(gu):
         i = gu.shape[-1] // 2
@@ -196,5 +243,5 @@ def test_certify_refuses_a_mismatch(small, monkeypatch):
 
     monkeypatch.setattr(engine_mod.tw, "silu_mul", wrong)
     with pytest.raises(RuntimeError, match=r"step\.norm_gate_up_swiglu.*silu_mul"):
-        eng._certify(2, 1)
-    assert (2, 1) not in eng.certified
+        eng.certify(eng.state.groups[0], 1)
+    assert (2, 1) not in eng.state.certified

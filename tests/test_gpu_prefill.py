@@ -1,0 +1,158 @@
+"""GPU parity of the prompt forward (``engine/engine.py:1123-1221``): the projection GEMM over many
+rows (``qwen_gemm``), causal chunk attention (``qwen_attn_prefill``) and the engine's chunked
+prompt forward, against the CPU oracle on the same inputs.
+
+Bars: GEMMs at the reference's op-certification tolerance (atol 1e-2, rtol 1/64,
+``engine/engine.py:425-429``) plus a two-hot case whose expected bits are closed-form (exact);
+attention atol 2e-2 (``tests/test_torch_ref.py:264``); the engine's per-layer hidden states within
+2e-2 relative and its first token under the greedy rule (the oracle's argmax unless its top-2 gap
+is below 1e-2).
+"""
+
+import pytest
+import torch
+
+from __graft_entry__ import write_random_model
+from helpers import assert_close
+from oracle import ref_torch as R
+from oracle.model import QWEN3_4B, CpuQwen3
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def qops():
+    from qwen_hip import ops
+    return ops
+
+
+def _bf16(*shape, gen, scale=1.0):
+    return (torch.randn(*shape, generator=gen, dtype=torch.float32) * scale).to(BF16)
+
+
+# ---------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (100, 256, 128), (255, 6144, 2560), (257, 2560, 4096),
+                                   (600, 2560, 9728), (2048, 1536, 512)])
+@pytest.mark.parametrize("kind", ["plain", "res", "silu"])
+def test_gemm_matches_oracle(qops, M, N, K, kind):
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    if kind == "silu" and N % 256:
+        pytest.skip("SwiGLU needs gate/up tile pairs in every 128-row tile")
+    x = _bf16(M, K, gen=g)
+    w = _bf16(N, K, gen=g, scale=0.03)
+    y = R.linear(x, w)
+    if kind == "silu":
+        want = R.silu_mul(y)
+    elif kind == "res":
+        resid = _bf16(M, N, gen=g)
+        want = (resid.float() + y.float()).to(BF16)
+    else:
+        want = y
+    t = qops.tile_weight(w.to(DEV), pair=kind == "silu")
+    if kind == "res":
+        out = resid.to(DEV)
+        got = qops.gemm(x.to(DEV), t, residual=out, out=out).cpu()     # in place, as the engine runs it
+    else:
+        got = qops.gemm(x.to(DEV), t, silu_pair=kind == "silu").cpu()
+    assert_close(got, want, 1e-2, 1 / 64, f"{kind} M={M} N={N} K={K}")
+
+
+def test_gemm_two_hot_exact(qops):
+    """Each output is a sum of two exactly representable products: exact in any order, so the
+    expected bf16 bits are closed-form (``engine/kernels/gemm_fused.py:227-277``); M spans a
+    partial row tile."""
+    M, N, K = 300, 256, 512
+    g = torch.Generator().manual_seed(23)
+    x = torch.randint(-8, 9, (M, K), generator=g).to(BF16)
+    w = torch.zeros(N, K, dtype=BF16)
+    cols = torch.randint(0, K, (N, 2), generator=g)
+    for n in range(N):
+        w[n, cols[n, 0]] += 0.5
+        w[n, cols[n, 1]] += 0.25
+    want = (x.double() @ w.double().T).to(BF16)
+    got = qops.gemm(x.to(DEV), qops.tile_weight(w.to(DEV))).cpu()
+    assert torch.equal(got, want)
+
+
+def test_gemm_rejects_bad_shapes(qops):
+    t = qops.tile_weight(torch.zeros(64, 128, dtype=BF16, device=DEV))     # N = 64: not a multiple of 128
+    with pytest.raises(AssertionError):
+        qops.gemm(torch.zeros(4, 128, dtype=BF16, device=DEV), t)
+
+
+# ---------------------------------------------------------------- chunk attention
+
+@pytest.mark.parametrize("B,T,p0,Nkv", [(1, 1, 0, 8), (1, 5, 0, 8), (2, 16, 0, 2), (1, 100, 37, 8), (3, 64, 64, 2),
+                                        (2, 33, 500, 8), (1, 300, 1000, 1)])
+def test_attn_prefill_matches_oracle(qops, B, T, p0, Nkv):
+    g = torch.Generator().manual_seed(B * 1000 + T + p0)
+    D, CAP = 128, p0 + T + 40
+    Nq = 4 * Nkv
+    kc = _bf16(B, Nkv, CAP, D, gen=g)
+    vc = _bf16(B, Nkv, CAP, D, gen=g)
+    kc[:, :, p0 + T:] = float("nan")          # slots past the chunk are never read
+    vc[:, :, p0 + T:] = float("inf")
+    q = _bf16(B, T, Nq, D, gen=g, scale=2.0)
+    scale = D ** -0.5
+    got = qops.attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), p0, scale).cpu()
+    lengths = torch.full((B,), p0 + T, dtype=torch.int32)
+    want = R.attn_decode(q, kc, vc, lengths, scale)   # query t sees slots j < p0 + t + 1
+    assert torch.isfinite(got.float()).all()
+    assert_close(got, want, 2e-2, 2e-2, f"attn_prefill B={B} T={T} p0={p0}")
+
+
+def test_attn_prefill_first_query_sees_only_slot_zero(qops):
+    """Position 0 sees one key: its output is that key's value row exactly (softmax of one)."""
+    g = torch.Generator().manual_seed(3)
+    B, T, Nkv, D = 2, 20, 2, 128
+    kc, vc = _bf16(B, Nkv, 32, D, gen=g), _bf16(B, Nkv, 32, D, gen=g)
+    q = _bf16(B, T, 4 * Nkv, D, gen=g)
+    out = qops.attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), 0, D ** -0.5).cpu().view(B, T, 4 * Nkv, D)
+    for h in range(4 * Nkv):
+        assert torch.equal(out[:, 0, h], vc[:, h // 4, 0])
+
+
+# ---------------------------------------------------------------- engine prompt forward
+
+@pytest.fixture(scope="module")
+def qwen4b_two_layers(tmp_path_factory):
+    from engine import Engine
+    cfg = dict(QWEN3_4B, num_hidden_layers=2)
+    path = write_random_model(str(tmp_path_factory.mktemp("pf")), cfg, seed=0, std=0.02)
+    return Engine(path), CpuQwen3.random_init(cfg, seed=0, std=0.02), cfg
+
+
+@pytest.mark.parametrize("B,S,chunk", [(1, 128, None), (2, 300, 256), (1, 2048, None)])
+def test_engine_prefill_matches_oracle(qwen4b_two_layers, monkeypatch, B, S, chunk):
+    """Hidden states after each layer (rows of the last chunk), the K/V written for every prompt
+    position, and the first token. ``chunk``: prompt-forward rows per chunk (forces several
+    chunks, whose attention reads earlier chunks' keys from the cache)."""
+    import engine as engine_mod
+    eng, ref, cfg = qwen4b_two_layers
+    if chunk is not None:
+        monkeypatch.setitem(engine_mod.CONFIG, "prefill_tokens", chunk)
+    g = torch.Generator().manual_seed(S)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    first, hidden = eng.prefill_hidden(prompt.tolist())
+    ref.prepare(B, eng.CAP)
+    want = []
+    _, logits = ref.prefill(prompt, hidden=want, return_logits=True)
+    Tc = hidden[0].shape[0] // B
+    for l, (a, w) in enumerate(zip(hidden, want)):
+        a = a.float().cpu().view(B, Tc, -1)
+        w = w.float().view(B, S, -1)[:, S - Tc:]
+        rel = float((a - w).norm() / w.norm())
+        assert rel <= 2e-2, f"layer {l} hidden: relative error {rel}"
+        kc, vc = eng.state.k(l)[:, :, :S].float().cpu(), eng.state.v(l)[:, :, :S].float().cpu()
+        kr, vr = ref.k_cache[l][:, :, :S].float(), ref.v_cache[l][:, :, :S].float()
+        for name, x, y in (("K", kc, kr), ("V", vc, vr)):
+            rel = float((x - y).norm() / y.norm())
+            assert rel <= 2e-2, f"layer {l} {name} cache: relative error {rel}"
+    lg = logits.float()
+    top2 = lg.topk(2, dim=-1).values
+    ok = (lg.argmax(-1) == first.cpu()) | ((top2[:, 0] - top2[:, 1]) < 1e-2)
+    assert bool(ok.all()), (first, lg.argmax(-1))

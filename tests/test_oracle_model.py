@@ -99,3 +99,27 @@ def test_judge_gaps_zero_on_own_tokens(models):
     steps = list(ref.generate(ids.tolist(), 5))
     tokens = [[steps[n][b] for n in range(5)] for b in range(2)]
     assert float(ref.judge_gaps(ids.tolist(), tokens).max()) == 0.0
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize("B,S,N", [(1, 9, 12), (2, 17, 8)])
+def test_replay_logits_match_hf_judge_replay(models, B, S, N):
+    """``replay_logits`` is the reference judge's single teacher-forced forward
+    (``tests/local_check.py:254-272``): against HF's own replay on the same tokens, and
+    consistent with the oracle's step-by-step decoding of the same prefix."""
+    ref, hf = models
+    ids = _prompt(B, S, 40 + S)
+    steps = list(ref.generate(ids.tolist(), N))
+    tokens = [[steps[n][b] for n in range(N)] for b in range(B)]
+    tok = torch.tensor(tokens)
+    mine = ref.replay_logits(ids.tolist(), tokens).float()
+    assert mine.shape == (B, N, CFG["vocab_size"])
+    full = torch.cat([ids, tok], 1)
+    pred = hf(input_ids=full, use_cache=False, return_dict=True).logits[:, S - 1:S + N - 1].float()
+    assert float((mine - pred).abs().max()) <= 0.05
+    stepwise = ref.teacher_forced_logits(ids.tolist(), tokens).float()
+    assert float((mine - stepwise).abs().max()) <= 0.05
+    # the oracle's own greedy tokens are the replay's argmax wherever its top-2 gap is not a tie
+    top2 = mine.topk(2, dim=-1).values
+    tie = (top2[..., 0] - top2[..., 1]) < 1e-2
+    assert bool(((mine.argmax(-1) == tok) | tie).all())

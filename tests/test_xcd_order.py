@@ -17,7 +17,8 @@ from qwen_hip import ops
 
 
 def _stub(Nq, Nkv, D, H):
-    return types.SimpleNamespace(Nq=Nq, Nkv=Nkv, D=D, H=H, device=None)
+    spec = types.SimpleNamespace(Nq=Nq, Nkv=Nkv, D=D, H=H, qkv_width=(Nq + 2 * Nkv) * D)
+    return types.SimpleNamespace(spec=spec, device=None)
 
 
 def _group_of(row, Nq, Nkv, D):

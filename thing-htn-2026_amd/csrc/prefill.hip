@@ -1,0 +1,454 @@
+// Prompt-forward kernels: the projection GEMM over many rows and causal flash attention.
+//
+// The reference's prompt forward (engine/engine.py:1181-1221) runs cuBLAS GEMMs and SDPA
+// over B x S rows. Here the prompt goes through in position chunks of all sequences; per
+// layer these two kernels do the heavy work (norms, RoPE + cache write and the first-token
+// LM head are the decode path's kernels):
+//
+// pf_gemm_kernel<EPI>: out[M, N] = A[M, K] @ W[N, K]^T with bf16 operands, fp32
+//   accumulation and one bf16 rounding (engine/kernels/gemm.py:12-15), and the fused
+//   epilogues of the decode projections (engine/kernels/gemm_fused.py:5-19):
+//     STORE : out = bf16(acc)
+//     RES   : out = bf16(res + bf16(acc))              (residual may alias out)
+//     SWIGLU: out = bf16(bf16(silu(bf16(g))) * bf16(u)) for a pair-interleaved gate|up weight
+//   W is in the MFMA-B tile layout (weights.hip): tile (nt, kt) = 16 rows x 32 k, 1 KB,
+//   lane l = 16 q + r holding W[16 nt + r][32 kt + 8 q .. +8], i.e. exactly the B operand of
+//   v_mfma_f32_16x16x32_bf16, so B fragments are one 16-byte load per lane with no LDS.
+//   A workgroup (4 wavefronts) computes a 256-row x 128-column tile; wavefront (wm, wn)
+//   owns rows 128 wm .. +128 and n-tiles 4 wn .. +4 (8 x 4 accumulator tiles). A is staged
+//   through LDS in k-steps of 64 (double buffered, 16-byte chunk c of row r at slot
+//   c ^ (r % 8), so the A-fragment reads of 8 consecutive rows hit 8 different bank groups);
+//   the next k-step's A and B loads are issued before the current one's MFMAs. Workgroups
+//   walk the tile grid in groups of 8 row tiles per column tile, so the 8 workgroups that
+//   share a weight column tile run at the same time (one per XCD) and each XCD keeps one
+//   A row tile in its L2. The epilogue stages each wavefront's tile in LDS as bf16 and
+//   writes 16-byte chunks.
+//
+// pf_attn_kernel: causal GQA attention of the T queries of a chunk (positions p0 + t) over
+//   the cache slots [0, p0 + t] (engine/engine.py:1123-1179's SDPA, with the decode
+//   attention's rounding points, engine/kernels/torch_ref.py:168-227: fp32 scores times
+//   scale, probabilities rounded to bf16 for the value product, fp32 row sums, one final
+//   rounding). One workgroup per (sequence, KV head, 16 query tokens) holds the 64 query
+//   rows (16 tokens x the 4 heads of the group); wavefront w owns tokens 4w .. 4w + 3. K and
+//   V blocks of 64 keys are staged in LDS once per workgroup (double buffered, padded rows)
+//   and shared by the 4 wavefronts: S = Q K^T and O += P V on the matrix cores, online
+//   softmax in the accumulator layout, V^T fragments by ds_read_b64_tr_b16 (as in
+//   attention_mfma.hip). Workgroups with the most keys are launched first.
+#include "common.h"
+
+namespace {
+
+enum { PEPI_STORE = 0, PEPI_RES = 1, PEPI_SWIGLU = 2 };
+
+constexpr int PBM = 256;   // rows of A per workgroup
+constexpr int PBN = 128;   // weight rows (output columns before SwiGLU) per workgroup
+constexpr int PBK = 64;    // k per pipeline stage
+constexpr int PGM = 8;     // row tiles per group of the tile walk
+
+// 16 bytes held as a native vector: arrays of these stay in VGPRs (an array of the HIP uint4
+// struct is placed in scratch memory, and every load into it then waits at its store).
+typedef unsigned pv4 __attribute__((ext_vector_type(4)));
+
+struct PfGemmParams {
+  const bf16_t* a;    // [M, K] row-major
+  const bf16_t* w;    // tiled [N, K]
+  const bf16_t* res;  // [M, ldo] (RES; may alias out)
+  bf16_t* out;        // [M, ldo]
+  int M, N, K, ldo;
+  int mtiles, ntiles;
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(256, 2) pf_gemm_kernel(PfGemmParams p) {
+  __shared__ uint4 lds[2 * PBM * (PBK / 8)];  // 64 KB: A double buffer, then the epilogue tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int qq = lane >> 4, rr = lane & 15;
+
+  // tile walk: groups of PGM row tiles; inside a group the row tile varies fastest
+  const int id = blockIdx.x;
+  const int per_group = PGM * p.ntiles;
+  const int grp = id / per_group;
+  const int rem = id - grp * per_group;
+  const int gsz = min(PGM, p.mtiles - grp * PGM);
+  const int mt = grp * PGM + rem % gsz;
+  const int ntile = rem / gsz;
+  const long long m0 = (long long)mt * PBM;
+  const int KT = p.K / 32, KB = p.K / PBK;
+  const int nt0 = ntile * (PBN / 16) + wn * 4;  // this wavefront's first n-tile
+
+  // A staging: thread -> 16-byte column chunk ac of rows (tid >> 3) + 32 i (rows past M
+  // re-read row M - 1 and are never stored)
+  const int ac = tid & 7;
+  // (M * K < 2^31 is checked by the host: element offsets fit in 32 bits)
+  const bf16_t* abase = p.a + ac * 8;
+  int aoff[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) aoff[i] = (int)min(m0 + (tid >> 3) + 32 * i, (long long)p.M - 1) * p.K;
+  pv4 ast[8];
+  auto load_a = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ast[i] = *reinterpret_cast<const pv4*>(abase + aoff[i] + kb * PBK);
+  };
+  auto store_a = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = (tid >> 3) + 32 * i;
+      *reinterpret_cast<pv4*>(&lds[buf * (PBM * 8) + row * 8 + (ac ^ (row & 7))]) = ast[i];
+    }
+  };
+  const pv4* wb = reinterpret_cast<const pv4*>(p.w) + (long long)nt0 * KT * 64 + lane;
+  pv4 bcur[4][2], bnext[4][2];
+  auto load_b = [&](pv4 (&d)[4][2], int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) d[j][kt] = wb[((long long)j * KT + kb * 2 + kt) * 64];
+  };
+
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  load_a(0);
+  load_b(bcur, 0);
+  store_a(0);
+  __syncthreads();
+  for (int kb = 0; kb < KB; ++kb) {
+    // next stage's loads first (the last iteration re-reads its own stage: in bounds, unused)
+    const int kn = kb + 1 < KB ? kb + 1 : kb;
+    load_a(kn);
+    load_b(bnext, kn);
+    const uint4* abuf = lds + (kb & 1) * (PBM * 8);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const int row = wm * 128 + mb * 16 + rr;
+        const bf16x8_t af = as_bf16x8(abuf[row * 8 + ((kt * 4 + qq) ^ (row & 7))]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8_t, bcur[j][kt]),
+                                                               acc[mb][j], 0, 0, 0);
+      }
+    }
+    store_a((kb + 1) & 1);  // buffer last read one iteration ago (behind the barrier below)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) bcur[j][kt] = bnext[j][kt];
+    __syncthreads();
+  }
+
+  // ---- epilogue: wavefront tile -> bf16 in LDS (rows of 8 chunks of 16 bytes, chunk c of
+  // row r at slot c ^ (r % 8)), then 16-byte stores.
+  // Accumulator layout: acc[mb][j][i] = D[16 mb + 4 qq + i][16 j + rr] of the wavefront tile.
+  constexpr int OCOLS = EPI == PEPI_SWIGLU ? 32 : 64;  // output columns per wavefront
+  constexpr int CPR = OCOLS / 8;                        // 16-byte chunks per row
+  bf16_t* tile = reinterpret_cast<bf16_t*>(lds + wave * 1024);  // 16 KB per wavefront
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = mb * 16 + 4 * qq + i;
+      if constexpr (EPI == PEPI_SWIGLU) {
+#pragma unroll
+        for (int pj = 0; pj < 2; ++pj) {
+          const float g = rbf(acc[mb][2 * pj][i]);
+          const float u = rbf(acc[mb][2 * pj + 1][i]);
+          const float s = rbf(g / (1.0f + expf(-g)));
+          const int col = pj * 16 + rr;
+          tile[row * 64 + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = f2bf(mul_rn(s, u));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = j * 16 + rr;
+          tile[row * 64 + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = f2bf(acc[mb][j][i]);
+        }
+      }
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  const long long col0 = EPI == PEPI_SWIGLU ? (long long)(nt0 / 2) * 16 : (long long)nt0 * 16;
+#pragma unroll 4
+  for (int c = lane; c < 128 * CPR; c += 64) {
+    const int row = c / CPR, ch = c - row * CPR;
+    const long long grow = m0 + wm * 128 + row;
+    const uint4 v = *reinterpret_cast<const uint4*>(tile + row * 64 + ((ch ^ (row & 7)) << 3));
+    if (grow < p.M) {
+      bf16_t* dst = p.out + grow * p.ldo + col0 + ch * 8;
+      if constexpr (EPI == PEPI_RES) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(p.res + grow * p.ldo + col0 + ch * 8);
+        float a[8], r[8];
+        unpack8(v, a);
+        unpack8(rv, r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = add_rn(r[e], a[e]);
+        *reinterpret_cast<uint4*>(dst) = pack8(a);
+      } else {
+        *reinterpret_cast<uint4*>(dst) = v;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ causal flash attention
+constexpr int AD = 128;      // head dim
+constexpr int AG = 4;        // query heads per KV head
+constexpr int AQ = 16;       // query tokens per workgroup
+constexpr int AKB = 64;      // keys per block
+constexpr int AKROW = 136;   // bf16 per LDS row of K (272 B)
+constexpr int AVROW = 144;   // bf16 per LDS row of V (288 B: banked transpose reads)
+constexpr float ANEG = -1e30f;
+
+typedef short av4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) av4i16 lds_av4i16;
+
+struct PfAttnParams {
+  const bf16_t* q;   // [B, T, Nq, D] (normed + rotated)
+  const bf16_t* kc;  // [B, Nkv, CAP, D]
+  const bf16_t* vc;
+  bf16_t* out;       // [B, T, Nq * D]
+  int T, Nkv, CAP, p0, qblocks;
+  long long bh_count;
+  float scale;
+};
+
+struct PfAttnSmem {
+  bf16_t k[2][AKB][AKROW];
+  bf16_t v[2][AKB][AVROW];
+  bf16_t pm[4][16][AKB];
+};
+
+template <int CTRL>
+__device__ __forceinline__ float pdpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float prow16_max(float v) {
+  v = fmaxf(v, pdpp<0xB1>(v));
+  v = fmaxf(v, pdpp<0x4E>(v));
+  v = fmaxf(v, pdpp<0x141>(v));
+  v = fmaxf(v, pdpp<0x140>(v));
+  return v;
+}
+__device__ __forceinline__ float prow16_sum(float v) {
+  v += pdpp<0xB1>(v);
+  v += pdpp<0x4E>(v);
+  v += pdpp<0x141>(v);
+  v += pdpp<0x140>(v);
+  return v;
+}
+
+__global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
+  __shared__ PfAttnSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qq = lane >> 4, rr = lane & 15;
+  // heaviest query blocks first
+  const long long id = blockIdx.x;
+  const int qb = p.qblocks - 1 - (int)(id / p.bh_count);
+  const long long bh = id % p.bh_count;
+  const long long b = bh / p.Nkv;
+  const int kvh = (int)(bh - b * p.Nkv);
+  const int T = p.T, Nq = p.Nkv * AG;
+  const int t_lo = qb * AQ;
+  const int kmax = p.p0 + min(T, t_lo + AQ);  // keys [0, kmax) are visible to some query here
+  const int nblk = (kmax + AKB - 1) / AKB;
+  const bf16_t* kbase = p.kc + bh * (long long)p.CAP * AD;
+  const bf16_t* vbase = p.vc + bh * (long long)p.CAP * AD;
+
+  // Q A-operand fragments: lane (q, r) holds row r of this wavefront's tile (token
+  // 4 wave + r / 4, head r % 4), dims 32 kt + 8 q .. +8. Tokens past T re-read token T - 1.
+  bf16x8_t qa[4];
+  {
+    const int t = min(t_lo + 4 * wave + (rr >> 2), T - 1);
+    const bf16_t* qr = p.q + (((b * T + t) * Nq) + kvh * AG + (rr & 3)) * (long long)AD + 8 * qq;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) qa[kt] = as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * kt));
+  }
+  // accumulator rows 4 qq + i: token t_lo + 4 wave + qq, head i; its last visible key
+  const int my_tok = t_lo + 4 * wave + qq;
+  const int my_last = p.p0 + my_tok;
+
+  // K / V staging: thread -> 16-byte chunk c of keys (tid >> 4) + 16 i (keys past kmax are
+  // read from slot 0 and their V rows zeroed, so a stale or non-finite slot never enters)
+  const int sc = tid & 15;
+  pv4 kst[4], vst[4];
+  auto load_kv = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = blk * AKB + (tid >> 4) + 16 * i;
+      const long long off = (long long)(key < kmax ? key : 0) * AD + sc * 8;
+      kst[i] = *reinterpret_cast<const pv4*>(kbase + off);
+      vst[i] = *reinterpret_cast<const pv4*>(vbase + off);
+    }
+  };
+  auto store_kv = [&](int buf, int blk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kr = (tid >> 4) + 16 * i;
+      const bool live = blk * AKB + kr < kmax;
+      *reinterpret_cast<pv4*>(&sm.k[buf][kr][sc * 8]) = kst[i];
+      *reinterpret_cast<pv4*>(&sm.v[buf][kr][sc * 8]) = live ? vst[i] : pv4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  float m[4], l[4];
+  f32x4_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { m[i] = ANEG; l[i] = 0.f; }
+#pragma unroll
+  for (int nd = 0; nd < 8; ++nd) o[nd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  bf16_t* pl = &sm.pm[wave][0][0];
+
+  load_kv(0);
+  store_kv(0, 0);
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int nb = blk + 1 < nblk ? blk + 1 : blk;
+    load_kv(nb);
+    const int buf = blk & 1;
+    const int kb0 = blk * AKB;
+    // S = Q K^T for 4 tiles of 16 keys: lane (q, r) takes key 16 nt + r, dims 32 kt + 8 q ..
+    f32x4_t s[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      s[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(&sm.k[buf][16 * nt + rr][32 * kt + 8 * qq]);
+        s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kt], as_bf16x8(kf), s[nt], 0, 0, 0);
+      }
+    }
+    // online softmax (rows 4 qq + i share the token, so one causal limit per lane)
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sv[4];
+      float mx = ANEG;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const bool vis = kb0 + 16 * nt + rr <= my_last;
+        sv[nt] = vis ? s[nt][i] * p.scale : ANEG;
+        mx = fmaxf(mx, sv[nt]);
+      }
+      mx = prow16_max(mx);
+      const float mn = fmaxf(m[i], mx);
+      alpha[i] = __expf(m[i] - mn);
+      float psum = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const float pr = sv[nt] > ANEG ? __expf(sv[nt] - mn) : 0.f;
+        psum += pr;
+        pl[(4 * qq + i) * AKB + 16 * nt + rr] = f2bf(pr);  // P rounded to bf16 for PV
+      }
+      l[i] = l[i] * alpha[i] + psum;
+      m[i] = mn;
+    }
+#pragma unroll
+    for (int nd = 0; nd < 8; ++nd)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[nd][i] *= alpha[i];
+    // P in the A layout (lane (q, r): row r, keys 32 kk + 8 q ..); the round trip stays inside
+    // the wavefront (LDS instructions complete in order)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    bf16x8_t pa[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) pa[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(pl + rr * AKB + 32 * kk + 8 * qq));
+    // O += P V: V^T fragments by transpose reads, source lane s -> V[8 q + s / 4 (+4)][16 nd + 4 (s % 4)]
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const bf16_t* vs = &sm.v[buf][32 * kk + 8 * qq + (rr >> 2)][4 * (rr & 3)];
+#pragma unroll
+      for (int nd = 0; nd < 8; ++nd) {
+        const av4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 16 * nd));
+        const av4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 4 * AVROW + 16 * nd));
+        const uint4 vv = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                    __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+        o[nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[kk], as_bf16x8(vv), o[nd], 0, 0, 0);
+      }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    store_kv(buf ^ 1, nb);  // buffer last read one iteration ago (behind the barrier below)
+    __syncthreads();
+  }
+
+  // ---- normalise and write: the wavefront's 16 rows x 128 dims through LDS (bf16), 16-byte stores
+#pragma unroll
+  for (int i = 0; i < 4; ++i) l[i] = prow16_sum(l[i]);
+  bf16_t* ot = &sm.k[0][0][0] + wave * 16 * AKROW;  // 16 rows of 272 B per wavefront
+#pragma unroll
+  for (int nd = 0; nd < 8; ++nd)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ot[(4 * qq + i) * AKROW + 16 * nd + rr] = f2bf(o[nd][i] / l[i]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = lane + 64 * it;        // 16 rows x 16 chunks
+    const int row = c >> 4, ch = c & 15;
+    const int t = t_lo + 4 * wave + (row >> 2);
+    if (t < T) {
+      const uint4 v = *reinterpret_cast<const uint4*>(ot + row * AKROW + ch * 8);
+      bf16_t* dst = p.out + ((b * T + t) * Nq + kvh * AG + (row & 3)) * (long long)AD + ch * 8;
+      *reinterpret_cast<uint4*>(dst) = v;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwen_gemm(const void* a, const void* w_tiled, void* out, int M, int N, int K, int ld_out, const void* residual,
+              int epi, hipStream_t stream) {
+  if (!a || !w_tiled || !out) return QWEN_ENULL;
+  if (M < 0 || N <= 0 || K <= 0 || N % PBN || K % PBK || epi < PEPI_STORE || epi > PEPI_SWIGLU) return QWEN_EARG;
+  const int ncols = epi == PEPI_SWIGLU ? N / 2 : N;
+  if (ld_out < ncols || ld_out % 8) return QWEN_EARG;
+  if (epi == PEPI_RES && !residual) return QWEN_ENULL;
+  if (M == 0) return QWEN_OK;
+  if ((long long)M * K >= 0x7fffffffLL) return QWEN_EARG;
+  PfGemmParams p{};
+  p.a = (const bf16_t*)a;
+  p.w = (const bf16_t*)w_tiled;
+  p.res = (const bf16_t*)residual;
+  p.out = (bf16_t*)out;
+  p.M = M; p.N = N; p.K = K; p.ldo = ld_out;
+  p.mtiles = (M + PBM - 1) / PBM;
+  p.ntiles = N / PBN;
+  const long long blocks = (long long)p.mtiles * p.ntiles;
+  if (blocks > 0x7fffffffLL) return QWEN_EARG;
+  const dim3 grid((unsigned)blocks);
+  if (epi == PEPI_STORE) pf_gemm_kernel<PEPI_STORE><<<grid, 256, 0, stream>>>(p);
+  else if (epi == PEPI_RES) pf_gemm_kernel<PEPI_RES><<<grid, 256, 0, stream>>>(p);
+  else pf_gemm_kernel<PEPI_SWIGLU><<<grid, 256, 0, stream>>>(p);
+  QWEN_RETURN_LAUNCH();
+}
+
+int qwen_attn_prefill(const void* q, const void* k_cache, const void* v_cache, void* out, int B, int T, int Nq,
+                      int Nkv, int D, int CAP, int p0, float scale, hipStream_t stream) {
+  if (!q || !k_cache || !v_cache || !out) return QWEN_ENULL;
+  if (D != AD || Nkv <= 0 || Nq != AG * Nkv || B < 0 || T < 0 || p0 < 0 || CAP <= 0) return QWEN_EARG;
+  if ((long long)p0 + T > CAP) return QWEN_EARG;
+  if (B == 0 || T == 0) return QWEN_OK;
+  PfAttnParams p{};
+  p.q = (const bf16_t*)q;
+  p.kc = (const bf16_t*)k_cache;
+  p.vc = (const bf16_t*)v_cache;
+  p.out = (bf16_t*)out;
+  p.T = T; p.Nkv = Nkv; p.CAP = CAP; p.p0 = p0;
+  p.qblocks = (T + AQ - 1) / AQ;
+  p.bh_count = (long long)B * Nkv;
+  p.scale = scale;
+  const long long blocks = p.bh_count * p.qblocks;
+  if (blocks > 0x7fffffffLL) return QWEN_EARG;
+  pf_attn_kernel<<<dim3((unsigned)blocks), 256, 0, stream>>>(p);
+  QWEN_RETURN_LAUNCH();
+}
+
+}  // extern "C"

@@ -1,49 +1,43 @@
 """Qwen3-4B greedy-decode engine for one MI355X (gfx950): drop-in for the reference's ``engine/engine.py``.
 
-Same public surface as the reference (``engine/engine.py:109-111``,
-``:1225-1250``): ``Engine(model_path)`` loads the model once; then
-``generate(input_ids, max_new_tokens)`` is a generator that yields exactly
-``max_new_tokens`` lists of ``B`` Python ints, the first from the prompt
-forward, then one per decode step. State resets on every call; batch size and
-prompt length may change between calls.
+Public surface as in the reference (``engine/engine.py:109-111``, ``:1225-1250``):
+``Engine(model_path)`` loads the model once; ``generate(input_ids, max_new_tokens)`` is a
+generator yielding exactly ``max_new_tokens`` lists of ``B`` Python ints, the first from the
+prompt forward, then one per decode step. State resets on every call; batch size and prompt
+length may change between calls.
 
-Per decode step the device runs only hand-written HIP kernels from
-``qwen_hip`` (libqwen_hip.so), recorded once per batch shape into one HIP
-graph (``torch.cuda.CUDAGraph``) and replayed per token:
+Device work is hand-written HIP kernels only (``qwen_hip``, ``libqwen_hip.so``):
 
-    36 x [ norm+QKV GEMM |
-           QK-norm + RoPE + KV write + split-K attention + merge |
-           O GEMM + residual | norm+gate/up GEMM+SwiGLU |
-           down GEMM + residual ]                      5 kernels / layer
-    final norm + LM head + argmax                      1 kernel
-    token / history / position update + next embedding 1 kernel
+* decode step (one HIP graph per step width ``T``, replayed per token), per row group of at
+  most 32 sequences::
 
-With ``CONFIG["spec_k"] = k > 0`` (exact speculative decoding, off by default as in
-the reference) a second graph verifies k prompt-lookup drafts per sequence in one
-T = k + 1 step: draft kernel | the same per-layer kernels over B*T rows | accept
-kernel (history scatter, position advance, next input row); the decode loop picks
-verify or plain steps adaptively.
+      36 x [ norm+QKV projection | QK-norm + RoPE + KV write + split attention + merge |
+             O projection + residual | norm + gate/up projection + SwiGLU |
+             down projection + residual ]
+      final norm + LM head + argmax | token / history / position update + next embedding
 
-Torch is used for device memory, the KV cache, the RoPE tables, graph
-capture, host<->device copies and (for now) the prompt forward's large GEMMs
-and causal attention (hipBLASLt / SDPA flash), whose norms, RoPE, cache writes
-and SwiGLU are the same HIP kernels. There is no CPU fallback: without a GPU
-or without libqwen_hip.so the constructor raises.
+* prompt forward: the prompt in position chunks of all sequences; per layer RMSNorm, the
+  MFMA GEMM over the tiled weights (QKV, O + residual, gate/up + SwiGLU, down + residual),
+  QK-norm + RoPE + KV write, and causal flash attention over the cache.
+
+Torch provides device memory, the RoPE tables, graph recording and host <-> device copies.
+There is no CPU path: without a GPU or without ``libqwen_hip.so`` the constructor raises.
+The host runtime (batch state, graphs, speculation policy, token pump) is in
+``decode_runtime.py``.
 """
 
 from __future__ import annotations
 
-import glob
 import json
 import math
 import os
 import sys
 import time
-from collections import deque
+from dataclasses import dataclass
 
 import torch
-import torch.nn.functional as F
 
+import decode_runtime as rt
 from qwen_hip import ops
 from qwen_hip import twins as tw
 from qwen_hip.ops import TiledWeight
@@ -52,30 +46,32 @@ BF16 = torch.bfloat16
 
 CONFIG = {
     "graphs": True,          # replay one HIP graph per decode step
-    "pipeline_depth": 3,     # decode steps in flight ahead of the host yield (engine/engine.py:71)
-    "prefill_rows": 32768,   # max B*S rows per prompt-forward batch slice (engine/engine.py:72)
-    "cap_align": 64,         # KV-cache capacity alignment (engine/engine.py:73)
+    "inflight": 4,           # decode steps queued on the device ahead of the consumer
+    "prefill_tokens": 16384, # rows (sequences x positions) per prompt-forward chunk
+    "cap_round": 256,        # KV capacity granularity (a later call with a smaller need reuses the state)
+    "group_rows": 32,        # sequences per decode row group (the kernels take at most 32 rows)
     # Exact speculative decoding (engine/engine.py:79-82): prompt-lookup drafts of spec_k tokens
     # verified in one T = spec_k + 1 step; 0 = off (the reference's default).
     "spec_k": int(os.environ.get("QWEN_ENGINE_SPEC_K", "0")),
     "spec_n": 3,             # n-gram length of the draft lookup
     "spec_max_batch": 8,     # speculate only when B <= this (and B * (spec_k + 1) <= 32)
-    "spec_probe": (24, 6),   # while speculation loses: plain steps between probes, spec steps per probe
-    # Run each decode-step shape's kernels against the torch twins once at warmup and refuse
-    # to decode on a mismatch (engine/engine.py:407-486; the reference falls back instead).
+    "spec_policy": "adaptive",   # or "always"
+    "spec_backoff": (16, 256),   # plain steps before re-probing a losing speculation (doubles)
+    "spec_probe_len": 4,         # verify steps per probe
+    # Run each decode-step shape's kernels against the torch twins once before the first decode
+    # of that shape and refuse to decode on a mismatch (engine/engine.py:407-486 falls back instead).
     "certify": os.environ.get("QWEN_ENGINE_CERTIFY", "1") != "0",
     # M <= 2: order the QKV GEMV's weight rows so that each KV head's q / k / v rows are
     # produced on the XCD that runs that head's attention workgroup.
     "xcd_heads": os.environ.get("QWEN_ENGINE_XCD_HEADS", "1") != "0",
-    # Whole-KV-cache size up to which the decode attention reads K/V with cache-allocating
-    # loads (measured on MI355X: c2 527 -> 530 tok/s; non-temporal loads win at c4).
+    # Whole-KV-cache size up to which the decode attention reads K/V with cache-allocating loads.
     "kv_cached_max_bytes": int(os.environ.get("QWEN_ENGINE_KV_CACHED_MAX", str(128 << 20))),
     "log": True,
 }
 
-XCDS = 8   # MI355X: 8 XCDs, workgroup i of a launch runs on XCD i mod 8
+XCDS = 8   # MI355X: 8 XCDs; workgroup i of a launch runs on XCD i mod 8
 
-# Tensor ids of the counter-based random-init generator (one per HF weight).
+# Generator tensor ids of the counter-based random init (one per HF weight).
 _PROJ_IDS = {"q_proj": 0, "k_proj": 1, "v_proj": 2, "o_proj": 3, "gate_proj": 4, "up_proj": 5, "down_proj": 6}
 
 
@@ -94,456 +90,533 @@ def random_init_scale(std: float) -> float:
     return float(np.float32(std / math.sqrt((65536.0 * 65536.0 - 1.0) / 3.0)))
 
 
-class _Layer:
-    __slots__ = ("ln1", "w_qkv", "q_norm", "k_norm", "w_o", "ln2", "w_gu", "w_down",
-                 "r_qkv", "r_o", "r_gu", "r_down", "g_qkv")
+@dataclass(frozen=True)
+class ModelSpec:
+    """Model dimensions from an HF ``config.json`` (``engine/engine.py:128-141``)."""
+
+    H: int
+    I: int
+    V: int
+    L: int
+    Nq: int
+    Nkv: int
+    D: int
+    eps: float
+    theta: float
+    tied: bool
+
+    @classmethod
+    def from_config(cls, cfg: dict) -> "ModelSpec":
+        rope = cfg.get("rope_parameters") or {}
+        theta = cfg.get("rope_theta", rope.get("rope_theta"))
+        if theta is None:
+            raise RuntimeError("config.json has neither rope_theta nor rope_parameters.rope_theta")
+        if cfg.get("rope_scaling") is not None or rope.get("rope_type", "default") != "default":
+            raise RuntimeError("rope scaling is not supported by this engine")
+        H, Nq = cfg["hidden_size"], cfg["num_attention_heads"]
+        spec = cls(H=H, I=cfg["intermediate_size"], V=cfg["vocab_size"], L=cfg["num_hidden_layers"], Nq=Nq,
+                   Nkv=cfg["num_key_value_heads"], D=cfg.get("head_dim") or H // Nq,
+                   eps=float(cfg["rms_norm_eps"]), theta=float(theta),
+                   tied=bool(cfg.get("tie_word_embeddings", False)))
+        if spec.D != 128 or spec.Nq != 4 * spec.Nkv:
+            raise RuntimeError(f"kernels need head_dim 128 and 4 query heads per KV head (got {spec.D}, "
+                               f"{spec.Nq}/{spec.Nkv})")
+        if spec.H % 512 or spec.I % 512 or spec.V % 16 or (spec.Nq * spec.D) % 512:
+            raise RuntimeError("hidden / intermediate / attention widths must be multiples of 512, vocab of 16")
+        return spec
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.Nq + 2 * self.Nkv) * self.D
+
+
+class LayerWeights:
+    """One decoder layer on the device: RMSNorm gains, the four projections in MFMA-B tiles
+    (decode at M > 2 and the prompt forward), and row-major copies for the M <= 2 GEMV."""
+
+    __slots__ = ("ln1", "ln2", "q_norm", "k_norm", "qkv", "o", "gu", "down",
+                 "qkv_rows", "o_rows", "gu_rows", "down_rows")
+
+
+class Weights:
+    """Device weights: layers, the embedding table (tiled; the gather reads it), the LM head
+    (tiled for M > 2, row-major for the GEMV) and the final norm. With tied embeddings the LM
+    head's tiled copy is the embedding table itself (``engine/engine.py:225-226``)."""
+
+    def __init__(self):
+        self.layers: list[LayerWeights] = []
+        self.embed: TiledWeight | None = None
+        self.lm: TiledWeight | None = None
+        self.lm_rows: torch.Tensor | None = None
+        self.final_norm: torch.Tensor | None = None
+        self.qkv_perm: torch.Tensor | None = None   # int64 [N]: row p of qkv_rows is natural row perm[p]
+        self.qkv_map: torch.Tensor | None = None    # the same permutation, int32 on the device
+
+    def natural_qkv_rows(self, w: LayerWeights) -> torch.Tensor:
+        """The row-major q|k|v weight in the HF order (undoing the XCD row order)."""
+        if self.qkv_perm is None:
+            return w.qkv_rows
+        out = torch.empty_like(w.qkv_rows)
+        out.index_copy_(0, self.qkv_perm.to(out.device), w.qkv_rows)
+        return out
+
+
+class StepBuffers:
+    """Activation buffers, launch shapes and workspaces of one decode step over one row group
+    (``rows`` sequences x ``T`` tokens); reused by every replay of that step."""
+
+    def __init__(self, spec: ModelSpec, rows: int, T: int, cap: int, device):
+        M = rows * T
+        self.rows, self.T, self.M = rows, T, M
+        self.h = torch.zeros((M, spec.H), dtype=BF16, device=device)
+        self.psq = torch.zeros((M, spec.H // 16), dtype=torch.float32, device=device)
+        self.qkv = torch.empty((M, spec.qkv_width), dtype=BF16, device=device)
+        self.a = torch.empty((rows, T, spec.Nq * spec.D), dtype=BF16, device=device)
+        self.p = torch.empty((M, spec.I), dtype=BF16, device=device)
+        self.nxt = torch.empty((M,), dtype=torch.int64, device=device)
+        self.tok = torch.zeros((rows, T), dtype=torch.int64, device=device)      # verify-step input ids
+        self.out_t = torch.zeros((T, rows), dtype=torch.int64, device=device)    # verify-step tokens [T, rows]
+        self.adv = torch.zeros((rows,), dtype=torch.int64, device=device)        # tokens accepted per row
+        self.keys = ops.argmax_keys(M, device)
+        self.mfma_attn = T <= ops.MFMA_MAX_T
+        self.splits = (ops.choose_mfma_splits(rows, spec.Nkv, cap) if self.mfma_attn
+                       else ops.choose_num_splits(rows, spec.Nkv, cap, T))
+        self.attn_waves = ops.MFMA_WAVES if self.mfma_attn else ops.attn_waves(rows, T)
+        self.attn_ws = (ops.attn_mfma_workspace(rows, T, spec.Nkv, self.splits, device) if self.mfma_attn
+                        else ops.attn_workspace(rows, T, spec.Nq, spec.Nkv, spec.D, self.splits, device))
+        self.cfg = {
+            "qkv": ops.gemm_config(M, spec.qkv_width, spec.H),
+            "o": ops.gemm_config(M, spec.H, spec.Nq * spec.D),
+            "gu": ops.gemm_config(M, 2 * spec.I, spec.H, True),
+            "down": ops.gemm_config(M, spec.H, spec.I),
+        }
+        widths = {"qkv": spec.qkv_width, "o": spec.H, "gu": 2 * spec.I, "down": spec.H}
+        ws = max(ops.gemm_workspace_bytes(M, widths[k], c) for k, c in self.cfg.items())
+        self.gemm_ws = ops.linear_workspace(ws, device)
+        self.gemv = M <= ops.GEMV_MAX_M
+        self.gemv_cfg = {
+            "qkv": ops.gemv_config(M, spec.qkv_width, spec.H, ops.GEPI_STORE, device),
+            "o": ops.gemv_config(M, spec.H, spec.Nq * spec.D, ops.GEPI_RES, device),
+            "gu": ops.gemv_config(M, spec.I, spec.H, ops.GEPI_SWIGLU, device),
+            "down": ops.gemv_config(M, spec.H, spec.I, ops.GEPI_RES, device),
+            "lm": ops.gemv_config(M, spec.V, spec.H, ops.GEPI_ARGMAX, device),
+        } if self.gemv else None
+        self.lm_cfg = ops.lm_head_config(M, spec.V, spec.H)
 
 
 class Engine:
     def __init__(self, model_path: str) -> None:
-        """Load the model from ``model_path`` (HF checkpoint dir, or config + random_init.json)."""
+        """Load the model in ``model_path``: an HF checkpoint directory (``config.json`` +
+        ``*.safetensors``) or ``config.json`` + ``random_init.json`` (seeded random weights)."""
         t0 = time.time()
         if not torch.cuda.is_available():
             raise RuntimeError("Engine needs an MI355X GPU (HIP device); there is no CPU path")
         self.device = torch.device("cuda:0")
-        torch.backends.cuda.matmul.allow_tf32 = False
         with open(os.path.join(model_path, "config.json")) as handle:
-            cfg = json.load(handle)
-        self.cfg = cfg
-        self.H = cfg["hidden_size"]
-        self.I = cfg["intermediate_size"]
-        self.V = cfg["vocab_size"]
-        self.L = cfg["num_hidden_layers"]
-        self.Nq = cfg["num_attention_heads"]
-        self.Nkv = cfg["num_key_value_heads"]
-        self.D = cfg.get("head_dim") or self.H // self.Nq
-        self.eps = float(cfg["rms_norm_eps"])
-        theta = cfg.get("rope_theta")
-        if theta is None:
-            theta = (cfg.get("rope_parameters") or {}).get("rope_theta")
-        self.theta = float(theta)
-        self.scale = self.D ** -0.5
-        rope_params = cfg.get("rope_parameters") or {}
-        if cfg.get("rope_scaling") is not None or rope_params.get("rope_type", "default") != "default":
-            raise RuntimeError("rope_scaling is not supported by this engine")
-        if self.D != 128 or self.Nq != 4 * self.Nkv:
-            raise RuntimeError(f"kernels support head_dim 128 and 4 query heads per KV head (got {self.D}, "
-                               f"{self.Nq}/{self.Nkv})")
-        if self.H % 32 or self.I % 32 or self.V % 16:
-            raise RuntimeError("hidden/intermediate sizes must be multiples of 32 and vocab of 16")
-        self.ops = {
-            "rms_norm": ops.rms_norm,
-            "add_rms_norm": ops.add_rms_norm,
-            "silu_mul": ops.silu_mul,
-            "qk_norm_rope_cache": ops.qk_norm_rope_cache,
-            "attn_decode": ops.attn_decode,
-        }
-        self.B = self.CAP = 0
-        self.graphs = {}
-        self.certified = {}
-        self.kv_cached = False
-        self.step_ms = {}
-        self.sdpa_mode = None
-        self.decode_launches = 0   # decode steps launched since load (benchmarks read it)
-        self.spec_launches = 0     # of which speculative verify steps
-        self.spec_tokens = 0       # tokens the slowest unfinished row gained from them
-        self.k_active = 0          # draft tokens per verify step for the prepared batch (0: plain only)
-        self._load_weights(model_path)
-        self.qkv_map = None
-        if CONFIG["xcd_heads"]:
-            order = self._qkv_xcd_order()
-            if order is not None:
-                self.qkv_map = order.to(torch.int32).to(self.device)
-                idx = order.to(self.device)
-                for w in self.layers:
-                    w.g_qkv = w.r_qkv.index_select(0, idx).contiguous()
-        self._rope_max = 0
-        self._ensure_rope(8192)
+            self.cfg = json.load(handle)
+        self.spec = ModelSpec.from_config(self.cfg)
+        s = self.spec
+        self.eps, self.scale = s.eps, s.D ** -0.5
+        # The reference's operator table (engine/engine.py:257-263), all HIP kernels.
+        self.ops = {"rms_norm": ops.rms_norm, "add_rms_norm": ops.add_rms_norm, "silu_mul": ops.silu_mul,
+                    "qk_norm_rope_cache": ops.qk_norm_rope_cache, "attn_decode": ops.attn_decode}
+        self.w = Weights()
+        if os.path.exists(os.path.join(model_path, "random_init.json")):
+            with open(os.path.join(model_path, "random_init.json")) as handle:
+                rnd = json.load(handle)
+            self._init_random(int(rnd.get("seed", 0)), float(rnd.get("std", 0.02)),
+                              norm_std=float(rnd.get("norm_std", 0.0)))
+        else:
+            self._load_checkpoint(model_path)
+        self.state: rt.BatchState | None = None
+        self.counters = {"decode": 0, "verify": 0, "verify_gain": 0}
+        self.cos_tab = self.sin_tab = None
+        self._rope_rows = 0
+        self._rope_for(8192)
         torch.cuda.synchronize()
-        _log(f"loaded in {time.time() - t0:.1f}s: L={self.L} H={self.H} V={self.V}")
+        _log(f"loaded in {rt.log_time(t0)}: L={s.L} H={s.H} V={s.V} tied={s.tied}")
 
-    # ------------------------------------------------------------------ weights
+    # ================================================================== weights
     def _qkv_xcd_order(self):
-        """Row order of the QKV weight for the M <= 2 GEMV in which the workgroups of one XCD
-        produce exactly one KV head group (its query heads, key and value rows), or None when
-        the shapes do not allow it.
+        """Row order of the M <= 2 QKV GEMV's weight in which the workgroups of one XCD produce
+        exactly one KV head group (its query heads, key and value rows), or None when the
+        shapes do not allow it.
 
         Workgroup g of a launch runs on XCD g mod 8, the GEMV's workgroup g owns weight rows
-        [N g / G, N (g + 1) / G), and the attention's workgroup for (sequence b, KV head h)
-        is number b * Nkv + h. With Nkv = 8 and each head group exactly G / 8 workgroups of
-        rows, permuting the rows as below (and storing each output at its natural column)
-        leaves head h's q / k / v rows in the L2 of the XCD whose attention workgroup reads
-        them. Returns ``orig [N]``: permuted row p is natural row orig[p]."""
-        N = (self.Nq + 2 * self.Nkv) * self.D
-        G, _ = ops.gemv_config(1, N, self.H, ops.GEPI_STORE, self.device)
-        qd = (self.Nq // self.Nkv) * self.D
-        grp = qd + 2 * self.D
-        if self.Nkv != XCDS or N % G or G % XCDS or grp != (G // XCDS) * (N // G):
+        [N g / G, N (g + 1) / G), and the decode attention's workgroup for (sequence b, KV
+        head h) is number b * Nkv + h. With Nkv = 8 and each head group exactly G / 8
+        workgroups of rows, the order below (outputs still stored at their natural columns)
+        leaves head h's q / k / v rows in the L2 of the XCD that runs its attention.
+        Returns ``perm [N]``: reordered row p is natural row perm[p]."""
+        s = self.spec
+        N = s.qkv_width
+        G, _ = ops.gemv_config(1, N, s.H, ops.GEPI_STORE, self.device)
+        qd = (s.Nq // s.Nkv) * s.D
+        grp = qd + 2 * s.D
+        if s.Nkv != XCDS or N % G or G % XCDS or grp != (G // XCDS) * (N // G):
             return None
         rows = N // G
         p = torch.arange(N, dtype=torch.int64)
         g, j = p // rows, p % rows
         h, i = g % XCDS, (g // XCDS) * rows + j
-        k0, v0 = self.Nq * self.D, (self.Nq + self.Nkv) * self.D
+        k0, v0 = s.Nq * s.D, (s.Nq + s.Nkv) * s.D
         return torch.where(i < qd, h * qd + i,
-                           torch.where(i < qd + self.D, k0 + h * self.D + (i - qd), v0 + h * self.D + (i - qd - self.D)))
+                           torch.where(i < qd + s.D, k0 + h * s.D + (i - qd), v0 + h * s.D + (i - qd - s.D)))
 
-    def _load_weights(self, model_path):
-        rnd = os.path.join(model_path, "random_init.json")
-        if os.path.exists(rnd):
-            with open(rnd) as handle:
-                spec = json.load(handle)
-            self._init_random(int(spec.get("seed", 0)), float(spec.get("std", 0.02)))
+    def _finish_layer(self, w: LayerWeights, qkv_rows: torch.Tensor):
+        """Store the QKV GEMV copy in the XCD row order (when enabled)."""
+        if self.w.qkv_perm is not None:
+            w.qkv_rows = qkv_rows.index_select(0, self.w.qkv_perm.to(self.device))
         else:
-            self._load_safetensors(model_path)
+            w.qkv_rows = qkv_rows
 
-    def _init_random(self, seed: int, std: float):
-        """Random-init weights on the device from the counter-based generator (tiled + row-major)."""
-        dev, H, I, D, Nq, Nkv = self.device, self.H, self.I, self.D, self.Nq, self.Nkv
+    def _init_random(self, seed: int, std: float, norm_std: float = 0.0):
+        """Seeded random weights written on the device by the counter-based generator
+        (``qwen_init_weight``): the tiled and row-major copies hold the same values. RMSNorm gains
+        are 1 (``Qwen3RMSNorm``'s init) unless ``norm_std > 0``, which draws them as
+        ``1 + N(0, norm_std)`` from a seeded torch generator (tests of non-unit gains)."""
+        s, dev = self.spec, self.device
         scale = random_init_scale(std)
-        ones_h = torch.ones(H, dtype=BF16, device=dev)
-        ones_d = torch.ones(D, dtype=BF16, device=dev)
-        self.layers = []
-        for l in range(self.L):
-            w = _Layer()
-            w.ln1, w.ln2, w.q_norm, w.k_norm = ones_h.clone(), ones_h.clone(), ones_d.clone(), ones_d.clone()
-            qkv_seg = ([0, Nq * D, (Nq + Nkv) * D],
-                       [_tid(l, "q_proj"), _tid(l, "k_proj"), _tid(l, "v_proj")])
-            gu_seg = ([0, I], [_tid(l, "gate_proj"), _tid(l, "up_proj")])
-            shapes = {
-                "qkv": ((Nq + 2 * Nkv) * D, H, qkv_seg, False),
-                "o": (H, Nq * D, ([0], [_tid(l, "o_proj")]), False),
-                "gu": (2 * I, H, gu_seg, True),
-                "down": (H, I, ([0], [_tid(l, "down_proj")]), False),
+        self.w.qkv_perm = self._qkv_xcd_order() if CONFIG["xcd_heads"] else None
+        if self.w.qkv_perm is not None:
+            self.w.qkv_map = self.w.qkv_perm.to(torch.int32).to(dev)
+        gen = torch.Generator().manual_seed(seed + 7)
+
+        def gain(n):
+            if norm_std <= 0:
+                return torch.ones(n, dtype=BF16, device=dev)
+            return (1.0 + norm_std * torch.randn(n, generator=gen)).to(BF16).to(dev)
+
+        qkv_seg = [0, s.Nq * s.D, (s.Nq + s.Nkv) * s.D]
+        for l in range(s.L):
+            w = LayerWeights()
+            w.ln1, w.ln2, w.q_norm, w.k_norm = gain(s.H), gain(s.H), gain(s.D), gain(s.D)
+            plan = {
+                "qkv": (s.qkv_width, s.H, qkv_seg, [_tid(l, "q_proj"), _tid(l, "k_proj"), _tid(l, "v_proj")], False),
+                "o": (s.H, s.Nq * s.D, [0], [_tid(l, "o_proj")], False),
+                "gu": (2 * s.I, s.H, [0, s.I], [_tid(l, "gate_proj"), _tid(l, "up_proj")], True),
+                "down": (s.H, s.I, [0], [_tid(l, "down_proj")], False),
             }
-            for name, (N, K, (starts, tids), pair) in shapes.items():
-                setattr(w, "w_" + name, TiledWeight.random(N, K, starts, tids, seed, scale, dev, pair))
-                row = torch.empty((N, K), dtype=BF16, device=dev)
-                ops.init_weight(row, N, K, False, False, starts, tids, seed, scale)
-                setattr(w, "r_" + name, row)
-            self.layers.append(w)
-        self.embed = TiledWeight.random(self.V, H, [0], [_tid(None, "embed")], seed, scale, dev)
-        self.embed_rows = torch.empty((self.V, H), dtype=BF16, device=dev)
-        ops.init_weight(self.embed_rows, self.V, H, False, False, [0], [_tid(None, "embed")], seed, scale)
-        self.final_norm = ones_h.clone()
+            for name, (N, K, starts, tids, pair) in plan.items():
+                setattr(w, name, TiledWeight.random(N, K, starts, tids, seed, scale, dev, pair))
+                rows = torch.empty((N, K), dtype=BF16, device=dev)
+                ops.init_weight(rows, N, K, False, False, starts, tids, seed, scale)
+                if name == "qkv":
+                    self._finish_layer(w, rows)
+                else:
+                    setattr(w, name + "_rows", rows)
+            self.w.layers.append(w)
+        self.w.embed = TiledWeight.random(s.V, s.H, [0], [_tid(None, "embed")], seed, scale, dev)
+        self.w.lm = self.w.embed
+        self.w.lm_rows = torch.empty((s.V, s.H), dtype=BF16, device=dev)
+        ops.init_weight(self.w.lm_rows, s.V, s.H, False, False, [0], [_tid(None, "embed")], seed, scale)
+        self.w.final_norm = gain(s.H)
 
-    def _load_safetensors(self, model_path):
-        """HF Qwen3 checkpoint (safetensors, safe loader) -> fused, tiled device weights."""
-        from safetensors.torch import safe_open
-        files = sorted(glob.glob(os.path.join(model_path, "*.safetensors")))
+    def _load_checkpoint(self, model_path: str):
+        """HF Qwen3 safetensors checkpoint -> device layouts (``engine/engine.py:184-230``).
+
+        Tensors are read one at a time with the safe loader (no pickle) and moved to the
+        device as bf16; q|k|v and gate|up are concatenated along the output dimension in
+        the reference's order. The LM head is the embedding when ``tie_word_embeddings`` is
+        set (a stored ``lm_head.weight`` is then ignored, as Transformers ties it), else the
+        checkpoint's ``lm_head.weight``."""
+        from safetensors import safe_open
+        s, dev = self.spec, self.device
+        files = sorted(f for f in os.listdir(model_path) if f.endswith(".safetensors"))
         if not files:
-            raise RuntimeError(f"no safetensors weights and no random_init.json in {model_path}")
-        tensors = {}
-        for f in files:
-            with safe_open(f, framework="pt", device="cpu") as handle:
-                for k in handle.keys():
-                    tensors[k] = handle.get_tensor(k)
+            raise RuntimeError(f"{model_path}: no *.safetensors weights and no random_init.json")
+        where = {}
+        handles = [safe_open(os.path.join(model_path, f), framework="pt", device="cpu") for f in files]
+        for hnd in handles:
+            for key in hnd.keys():
+                where[key] = hnd
 
-        def get(name):
-            return tensors[name].to(device=self.device, dtype=BF16).contiguous()
+        def get(name, shape):
+            if name not in where:
+                raise RuntimeError(f"{model_path}: checkpoint has no tensor {name}")
+            t = where[name].get_tensor(name)
+            if tuple(t.shape) != tuple(shape):
+                raise RuntimeError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+            return t.to(dtype=BF16).to(dev).contiguous()
 
-        self.layers = []
-        for l in range(self.L):
+        self.w.qkv_perm = self._qkv_xcd_order() if CONFIG["xcd_heads"] else None
+        if self.w.qkv_perm is not None:
+            self.w.qkv_map = self.w.qkv_perm.to(torch.int32).to(dev)
+        for l in range(s.L):
             p = f"model.layers.{l}."
-            w = _Layer()
-            w.ln1 = get(p + "input_layernorm.weight")
-            w.ln2 = get(p + "post_attention_layernorm.weight")
-            w.q_norm = get(p + "self_attn.q_norm.weight")
-            w.k_norm = get(p + "self_attn.k_norm.weight")
-            w.r_qkv = torch.cat([get(p + "self_attn.q_proj.weight"), get(p + "self_attn.k_proj.weight"),
-                                 get(p + "self_attn.v_proj.weight")], 0).contiguous()
-            w.r_o = get(p + "self_attn.o_proj.weight")
-            w.r_gu = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], 0).contiguous()
-            w.r_down = get(p + "mlp.down_proj.weight")
-            w.w_qkv = ops.tile_weight(w.r_qkv)
-            w.w_o = ops.tile_weight(w.r_o)
-            w.w_gu = ops.tile_weight(w.r_gu, pair=True)
-            w.w_down = ops.tile_weight(w.r_down)
-            self.layers.append(w)
-        emb = get("model.embed_tokens.weight")
-        self.embed = ops.tile_weight(emb)
-        self.embed_rows = emb          # row-major copy: the M <= 2 LM head streams it
-        if "lm_head.weight" in tensors and not self.cfg.get("tie_word_embeddings", True):
-            raise RuntimeError("untied LM head is not supported (Qwen3-4B ties it to the embedding)")
-        self.final_norm = get("model.norm.weight")
-        del tensors
+            w = LayerWeights()
+            w.ln1 = get(p + "input_layernorm.weight", (s.H,))
+            w.ln2 = get(p + "post_attention_layernorm.weight", (s.H,))
+            w.q_norm = get(p + "self_attn.q_norm.weight", (s.D,))
+            w.k_norm = get(p + "self_attn.k_norm.weight", (s.D,))
+            qkv = torch.cat([get(p + "self_attn.q_proj.weight", (s.Nq * s.D, s.H)),
+                             get(p + "self_attn.k_proj.weight", (s.Nkv * s.D, s.H)),
+                             get(p + "self_attn.v_proj.weight", (s.Nkv * s.D, s.H))], 0)
+            gu = torch.cat([get(p + "mlp.gate_proj.weight", (s.I, s.H)),
+                            get(p + "mlp.up_proj.weight", (s.I, s.H))], 0)
+            w.o_rows = get(p + "self_attn.o_proj.weight", (s.H, s.Nq * s.D))
+            w.down_rows = get(p + "mlp.down_proj.weight", (s.H, s.I))
+            w.gu_rows = gu
+            w.qkv = ops.tile_weight(qkv)
+            w.o = ops.tile_weight(w.o_rows)
+            w.gu = ops.tile_weight(gu, pair=True)
+            w.down = ops.tile_weight(w.down_rows)
+            self._finish_layer(w, qkv)
+            self.w.layers.append(w)
+        emb = get("model.embed_tokens.weight", (s.V, s.H))
+        self.w.embed = ops.tile_weight(emb)
+        if s.tied:
+            self.w.lm, self.w.lm_rows = self.w.embed, emb
+        else:
+            self.w.lm_rows = get("lm_head.weight", (s.V, s.H))
+            self.w.lm = ops.tile_weight(self.w.lm_rows)
+        self.w.final_norm = get("model.norm.weight", (s.H,))
+        del handles, where
+        torch.cuda.synchronize()
 
-    def _ensure_rope(self, max_pos):
-        """cos/sin ``[P, D]`` bf16 with the reference's op sequence (``engine/engine.py:232-251``).
-
-        Computed on the host CPU so the table is bit-identical to the
-        Transformers rotary embedding on CPU, then copied to the device.
-        """
-        if max_pos <= self._rope_max:
+    def _rope_for(self, positions: int):
+        """cos/sin ``[P, D]`` bf16 tables covering ``positions``, P a power of two >= 1024, with the
+        reference's op sequence (``engine/engine.py:232-251``) on the host CPU so they are
+        bit-identical to the Transformers rotary embedding, then copied to the device. A new
+        table invalidates recorded graphs (they hold the old addresses)."""
+        if positions <= self._rope_rows:
             return
-        P = int(2 ** math.ceil(math.log2(max(max_pos, 1024))))
-        inv_freq = 1.0 / (self.theta ** (torch.arange(0, self.D, 2, dtype=torch.int64).to(torch.float32) / self.D))
-        pos = torch.arange(P, dtype=torch.float32)[None, :]
-        freqs = (inv_freq[None, :, None].float().expand(1, -1, 1) @ pos[:, None, :].float()).transpose(1, 2)
+        s = self.spec
+        P = 1 << max(10, math.ceil(math.log2(max(positions, 1))))
+        inv = 1.0 / (s.theta ** (torch.arange(0, s.D, 2, dtype=torch.int64).to(torch.float32) / s.D))
+        t = torch.arange(P, dtype=torch.float32)[None, :]
+        freqs = (inv[None, :, None].float().expand(1, -1, 1) @ t[:, None, :].float()).transpose(1, 2)
         emb = torch.cat((freqs, freqs), dim=-1)
         self.cos_tab = emb.cos()[0].to(BF16).contiguous().to(self.device)
         self.sin_tab = emb.sin()[0].to(BF16).contiguous().to(self.device)
-        self._rope_max = P
-        self.graphs = {}  # captured graphs hold the old table addresses
+        self._rope_rows = P
+        if self.state is not None:
+            self.state.graphs = {}
 
-    # ------------------------------------------------------------------ state
-    def _prepare(self, B, S, N):
-        """Per-shape state (``engine/engine.py:830-863``): KV cache, history, buffers, graph."""
-        if B > 32:
-            raise ValueError("this engine decodes at most 32 sequences per call")
+    # ================================================================== state
+    @property
+    def B(self) -> int:
+        return self.state.B if self.state else 0
+
+    @property
+    def CAP(self) -> int:
+        return self.state.cap if self.state else 0
+
+    @property
+    def k_active(self) -> int:
+        return self.state.k if self.state else 0
+
+    def _spec_k_for(self, B: int) -> int:
         k = int(CONFIG["spec_k"])
-        if not (0 < k <= 15 and B <= CONFIG["spec_max_batch"] and B * (k + 1) <= 32):
-            k = 0
-        slack = (CONFIG["pipeline_depth"] + 3) * (k + 1) + 16
-        align = CONFIG["cap_align"]
-        cap = ((S + N + slack + align - 1) // align) * align
-        self._ensure_rope(cap)
-        if B != self.B or cap > self.CAP or k != getattr(self, "k_active", 0):
-            torch.cuda.synchronize()
-            self.graphs = {}
-            self.k_cache = self.v_cache = None
-            torch.cuda.empty_cache()
-            dev = self.device
-            shape = (B, self.Nkv, cap, self.D)
-            self.k_cache = [torch.zeros(shape, dtype=BF16, device=dev) for _ in range(self.L)]
-            self.v_cache = [torch.zeros(shape, dtype=BF16, device=dev) for _ in range(self.L)]
-            self.hist_buf = torch.zeros((B, cap), dtype=torch.int64, device=dev)
-            self.pos_buf = torch.zeros((B,), dtype=torch.int32, device=dev)
-            self.s_buf = torch.zeros((1,), dtype=torch.int64, device=dev)
-            self.ntarget_buf = torch.full((1,), 1 << 40, dtype=torch.int64, device=dev)
-            self.B, self.CAP, self.k_active = B, cap, k
-            self.certified = {}
-            # A KV cache well inside the 256 MB Infinity Cache stays there between steps when it
-            # is read with cache-allocating loads; larger ones stream with non-temporal loads.
-            kv_bytes = 2 * self.L * B * self.Nkv * cap * self.D * 2
-            self.kv_cached = kv_bytes <= CONFIG["kv_cached_max_bytes"]
-            self.bufs = {}
-            ring = CONFIG["pipeline_depth"] + 2
-            self.pin_nxt = [torch.zeros((k + 1, B), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
-            self.pin_adv = [torch.zeros((B,), dtype=torch.int64, pin_memory=True) for _ in range(ring)]
-            self.events = [torch.cuda.Event() for _ in range(ring)]
-            _log(f"state B={B} CAP={cap} spec_k={k} "
-                 f"kv={2 * self.L * B * self.Nkv * cap * self.D * 2 / 2**30:.2f}GiB")
-        for T in (1, k + 1) if k else (1,):
-            if CONFIG["certify"] and (B, T) not in self.certified:
-                self._certify(B, T)
-            if CONFIG["graphs"] and T not in self.graphs:
-                self._capture(T)
+        ok = 0 < k <= 15 and B <= CONFIG["spec_max_batch"] and B * (k + 1) <= 32
+        return k if ok else 0
 
-    def _buffers(self, B, T):
-        """Static activation buffers for a (B, T) step, reused by every replay."""
-        key = (B, T)
-        if key not in self.bufs:
-            M, dev = B * T, self.device
-            mfma = T <= ops.MFMA_MAX_T   # matrix-core attention for decode / verify widths
-            S = (ops.choose_mfma_splits(B, self.Nkv, self.CAP) if mfma
-                 else ops.choose_num_splits(B, self.Nkv, self.CAP, T))
-            W_qkv = (self.Nq + 2 * self.Nkv) * self.D
-            cfg = {
-                "qkv": ops.gemm_config(M, W_qkv, self.H),
-                "o": ops.gemm_config(M, self.H, self.Nq * self.D),
-                "gu": ops.gemm_config(M, 2 * self.I, self.H, True),
-                "down": ops.gemm_config(M, self.H, self.I),
-            }
-            n_of = {"qkv": W_qkv, "o": self.H, "gu": 2 * self.I, "down": self.H}
-            ws = max(ops.gemm_workspace_bytes(M, n_of[k], c) for k, c in cfg.items())
-            gemv = M <= ops.GEMV_MAX_M
-            gemv_cfg = {
-                "qkv": ops.gemv_config(M, W_qkv, self.H, ops.GEPI_STORE, dev),
-                "o": ops.gemv_config(M, self.H, self.Nq * self.D, ops.GEPI_RES, dev),
-                "gu": ops.gemv_config(M, self.I, self.H, ops.GEPI_SWIGLU, dev),
-                "down": ops.gemv_config(M, self.H, self.I, ops.GEPI_RES, dev),
-                "lm": ops.gemv_config(M, self.V, self.H, ops.GEPI_ARGMAX, dev),
-            } if gemv else None
-            self.bufs[key] = {
-                "h": torch.zeros((M, self.H), dtype=BF16, device=dev),
-                "qkv": torch.empty((M, W_qkv), dtype=BF16, device=dev),
-                "a": torch.empty((B, T, self.Nq * self.D), dtype=BF16, device=dev),
-                "p": torch.empty((M, self.I), dtype=BF16, device=dev),
-                "psq": torch.zeros((M, self.H // 16), dtype=torch.float32, device=dev),
-                "next": torch.empty((M,), dtype=torch.int64, device=dev),
-                "tok": torch.zeros((B, T), dtype=torch.int64, device=dev),      # verify-step input ids
-                "out_t": torch.zeros((T, B), dtype=torch.int64, device=dev),    # verify-step tokens, [T, B]
-                "adv": torch.zeros((B,), dtype=torch.int64, device=dev),        # accepted tokens per row
-                "keys": ops.argmax_keys(M, dev),
-                "attn_mfma": mfma,
-                "splits": S,
-                "attn_waves": ops.MFMA_WAVES if mfma else ops.attn_waves(B, T),
-                "attn_ws": (ops.attn_mfma_workspace(B, T, self.Nkv, S, dev) if mfma
-                            else ops.attn_workspace(B, T, self.Nq, self.Nkv, self.D, S, dev)),
-                "gemm_ws": ops.linear_workspace(ws, dev),
-                "cfg": cfg,
-                "gemv": gemv,
-                "gemv_cfg": gemv_cfg,
-                "lm_cfg": ops.lm_head_config(M, self.V, self.H),
-            }
-        return self.bufs[key]
+    def prepare(self, B: int, S: int, N: int) -> rt.BatchState:
+        """Batch state for ``B`` prompts of ``S`` tokens and ``N`` outputs: reused when the batch
+        size and draft length match and its capacity suffices, else rebuilt. Certifies and
+        records the decode steps of the shape (once per state)."""
+        k = self._spec_k_for(B)
+        cap = rt.capacity(S, N, k, CONFIG["cap_round"])
+        self._rope_for(cap)
+        st = self.state
+        if st is None or st.B != B or st.k != k or st.cap < cap:
+            self.state = None
+            if st is not None:
+                del st
+                torch.cuda.synchronize()
+                torch.cuda.empty_cache()
+            st = rt.BatchState(self.spec, B, cap, k, self.device, CONFIG["group_rows"])
+            st.kv_cached = st.kv_bytes <= CONFIG["kv_cached_max_bytes"]
+            self.state = st
+            _log(f"batch state B={B} cap={cap} groups={len(st.groups)} spec_k={k} kv={st.kv_bytes / 2**30:.2f}GiB")
+        for T in ((1, k + 1) if k else (1,)):
+            if CONFIG["certify"]:
+                for g in {st.groups[0].n: st.groups[0], st.groups[-1].n: st.groups[-1]}.values():
+                    if (g.n, T) not in st.certified:
+                        self.certify(g, T)
+            if CONFIG["graphs"] and T not in st.graphs:
+                issue = self._issue_plain if T == 1 else (lambda: self._issue_verify())
+                st.graphs[T] = rt.StepGraph(issue, st, T).record()
+                _log(f"recorded T={T} step graph: {st.graphs[T].ms:.3f} ms/step")
+        return st
 
-    # ------------------------------------------------------------------ decode step
-    def _step(self, T, tok=None, hidden=None):
-        """One decode step of ``T`` tokens per sequence (``engine/engine.py:1093-1121``).
+    def bufs(self, g: rt.RowGroup, T: int) -> StepBuffers:
+        st = self.state
+        key = (g.index, T)
+        if key not in st.bufs:
+            st.bufs[key] = StepBuffers(self.spec, g.n, T, st.cap, self.device)
+        return st.bufs[key]
 
-        With ``tok [B, T]`` int64 the step embeds those ids and returns the
-        greedy ``next [B*T]`` int64 buffer. Without it (T = 1, the plain step)
-        the input rows are already in ``h`` / ``psq`` (the embedding of
-        ``hist[b, pos[b]]``, left there by the previous step's tail or by
-        ``_prime``) and the argmax stays in the packed keys for ``decode_finish``.
-        Positions are ``pos_buf``; K/V are written at ``pos + t``. Issues only
-        HIP kernels and allocates nothing, so it is capturable.
-        """
-        B = self.B
-        M = B * T
-        b = self._buffers(B, T)
-        h, psq = b["h"], b["psq"]
-        # psq holds the per-16-column sums of squares of the current residual
-        # stream h: written by whoever last wrote h (embedding, O / down
-        # epilogues), read by the next normed projection.
-        if tok is not None:
-            ops.embed(tok.reshape(-1), self.embed, out=h, psq_out=psq)
-        else:
-            assert T == 1
-        for l in range(self.L):
-            self._layer(l, b, T)
-            if hidden is not None:
-                hidden.append(h.clone())
-        self._lm_head(b, M, extract=tok is not None)
-        return b["next"]
-
-    def _lm_head(self, b, M, extract):
-        """Final RMSNorm + tied LM head + argmax of the step buffers ``b`` (``engine/engine.py:1119-1121``):
-        tokens into ``b["next"]`` with ``extract``, else left in the packed keys for ``decode_finish``."""
-        if b["gemv_cfg"] is not None:
-            ops.gemv(b["h"], self.embed_rows, norm_w=self.final_norm, eps=self.eps, amax=b["keys"],
-                     cfg=b["gemv_cfg"]["lm"])
-            if extract:
-                ops.argmax_extract(b["keys"], M, b["next"])
-        else:
-            ops.lm_head_argmax(b["h"], self.final_norm, self.eps, self.embed, cfg=b["lm_cfg"],
-                               out=b["next"] if extract else None, keys=b["keys"], psq_in=b["psq"], extract=extract)
-
-    def _layer(self, l, b, T, trace=None):
-        """Decoder layer ``l`` of ``_step`` (``engine/engine.py:1103-1118``) on the step buffers
-        ``b``: the residual stream ``h`` (and its statistics ``psq``) is updated in place, K/V
-        are written at ``pos_buf + t``. ``trace`` (a list) receives copies of qkv, the attention
-        output, h after the O projection, the SwiGLU product and h after the down projection."""
-        M = self.B * T
-        w = self.layers[l]
-        h, qkv, a, p, psq, cfg, ws = b["h"], b["qkv"], b["a"], b["p"], b["psq"], b["cfg"], b["gemm_ws"]
-        gc = b["gemv_cfg"]
+    # ================================================================== decode step
+    def _layer(self, l: int, g: rt.RowGroup, b: StepBuffers, trace=None):
+        """Decoder layer ``l`` (``engine/engine.py:1103-1118``) on the step buffers ``b`` of row
+        group ``g``: the residual stream ``h`` (and its RMSNorm statistics ``psq``) is updated in
+        place, K/V are written at ``pos + t``. ``trace`` (a list) receives copies of qkv, the
+        attention output, h after O, the SwiGLU product and h after down."""
+        w, s = self.w.layers[l], self.spec
+        kc, vc = g.kv[l]
         keep = (lambda t: trace.append(t.clone())) if trace is not None else (lambda t: None)
-        # M <= 2: balanced row-major GEMVs (RMSNorm statistics computed in-kernel);
-        # larger M: MFMA kernels over the tiled weights, statistics from psq.
-        if gc is not None:
-            if self.qkv_map is not None:   # head h's rows produced on XCD h (see _qkv_xcd_order)
-                ops.gemv(h, w.g_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"], row_map=self.qkv_map)
-            else:
-                ops.gemv(h, w.r_qkv, norm_w=w.ln1, eps=self.eps, out=qkv, cfg=gc["qkv"])
+        M = b.M
+        # M <= 2: balanced row-major GEMVs (statistics computed in-kernel); else MFMA GEMMs over
+        # the tiled weights, statistics from psq (left by whoever last wrote h).
+        if b.gemv:
+            gc = b.gemv_cfg
+            ops.gemv(b.h, w.qkv_rows, norm_w=w.ln1, eps=s.eps, out=b.qkv, cfg=gc["qkv"], row_map=self.w.qkv_map)
         else:
-            ops.fused_linear(h, w.w_qkv, cfg["qkv"], norm_w=w.ln1, eps=self.eps, out=qkv, psq_in=psq, workspace=ws)
-        keep(qkv)
-        if b["attn_mfma"]:
-            ops.attn_decode_mfma(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
-                                 self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
-                                 workspace=b["attn_ws"], waves=b["attn_waves"], kv_cached=self.kv_cached)
+            ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=s.eps, out=b.qkv, psq_in=b.psq,
+                             workspace=b.gemm_ws)
+        keep(b.qkv)
+        if b.mfma_attn:
+            ops.attn_decode_mfma(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc, vc,
+                                 self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves,
+                                 kv_cached=self.state.kv_cached)
         else:
-            ops.attn_decode_fused(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, self.pos_buf, T,
-                                  self.k_cache[l], self.v_cache[l], self.scale, b["splits"], out=a,
-                                  workspace=b["attn_ws"], waves=b["attn_waves"])
-        keep(a)
-        if gc is not None:
-            ops.gemv(a.view(M, -1), w.r_o, residual=h, out=h, cfg=gc["o"])
-            keep(h)
-            ops.gemv(h, w.r_gu, norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p, cfg=gc["gu"])
-            keep(p)
-            ops.gemv(p, w.r_down, residual=h, out=h, cfg=gc["down"])
+            ops.attn_decode_fused(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc, vc,
+                                  self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves)
+        keep(b.a)
+        a = b.a.view(M, -1)
+        if b.gemv:
+            gc = b.gemv_cfg
+            ops.gemv(a, w.o_rows, residual=b.h, out=b.h, cfg=gc["o"])
+            keep(b.h)
+            ops.gemv(b.h, w.gu_rows, norm_w=w.ln2, eps=s.eps, silu_pair=True, out=b.p, cfg=gc["gu"])
+            keep(b.p)
+            ops.gemv(b.p, w.down_rows, residual=b.h, out=b.h, cfg=gc["down"])
         else:
-            ops.fused_linear(a.view(M, -1), w.w_o, cfg["o"], residual=h, out=h, psq_out=psq, workspace=ws)
-            keep(h)
-            ops.fused_linear(h, w.w_gu, cfg["gu"], norm_w=w.ln2, eps=self.eps, silu_pair=True, out=p,
-                             psq_in=psq, workspace=ws)
-            keep(p)
-            ops.fused_linear(p, w.w_down, cfg["down"], residual=h, out=h, psq_out=psq, workspace=ws)
-        keep(h)
+            ops.fused_linear(a, w.o, b.cfg["o"], residual=b.h, out=b.h, psq_out=b.psq, workspace=b.gemm_ws)
+            keep(b.h)
+            ops.fused_linear(b.h, w.gu, b.cfg["gu"], norm_w=w.ln2, eps=s.eps, silu_pair=True, out=b.p,
+                             psq_in=b.psq, workspace=b.gemm_ws)
+            keep(b.p)
+            ops.fused_linear(b.p, w.down, b.cfg["down"], residual=b.h, out=b.h, psq_out=b.psq, workspace=b.gemm_ws)
+        keep(b.h)
 
-    def layer_step(self, l: int, hidden: torch.Tensor, positions, T: int = 1) -> list:
-        """One decoder layer on a given residual stream ``hidden [B*T, H]`` at ``positions``
-        (the reference's single-layer case): returns the per-tensor trace of
-        ``_layer`` (qkv, attention output, h after O, SwiGLU product, h after down). Uses the
-        prepared batch and caches; eager, synchronous."""
-        assert hidden.shape == (self.B * T, self.H)
-        b = self._buffers(self.B, T)
-        trace = []
-        with torch.inference_mode():
-            self.pos_buf.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
-            b["h"].copy_(hidden.to(self.device, BF16))
-            ops.sumsq16(b["h"], out=b["psq"])
-            self._layer(l, b, T, trace=trace)
-        torch.cuda.synchronize()
-        return trace
+    def _lm_head(self, b: StepBuffers, extract: bool):
+        """Final RMSNorm + LM head + argmax (``engine/engine.py:1119-1121``): tokens into ``b.nxt``
+        with ``extract``, else left in the packed keys for the step tail."""
+        if b.gemv:
+            ops.gemv(b.h, self.w.lm_rows, norm_w=self.w.final_norm, eps=self.eps, amax=b.keys, cfg=b.gemv_cfg["lm"])
+            if extract:
+                ops.argmax_extract(b.keys, b.M, b.nxt)
+        else:
+            ops.lm_head_argmax(b.h, self.w.final_norm, self.eps, self.w.lm, cfg=b.lm_cfg,
+                               out=b.nxt if extract else None, keys=b.keys, psq_in=b.psq, extract=extract)
 
-    def _certify(self, B, T, seed=0):
+    def _forward_rows(self, g: rt.RowGroup, T: int, tok=None, hidden=None) -> StepBuffers:
+        """``_step`` (``engine/engine.py:1093-1121``) for row group ``g``: with ``tok [rows, T]`` the
+        ids are embedded and the greedy tokens land in ``b.nxt``; without (T = 1) the input rows
+        are already in ``h`` / ``psq`` and the argmax stays in the packed keys."""
+        b = self.bufs(g, T)
+        if tok is not None:
+            ops.embed(tok.reshape(-1), self.w.embed, out=b.h, psq_out=b.psq)
+        for l in range(self.spec.L):
+            self._layer(l, g, b)
+            if hidden is not None:
+                hidden.append(b.h.clone())
+        self._lm_head(b, extract=tok is not None)
+        return b
+
+    def _issue_plain(self):
+        """One plain step for every row group (``engine/engine.py:941-953``): each group runs on
+        the embedding of ``hist[pos]``; the tail writes the token, ``hist[pos + 1]``, advances
+        ``pos`` (frozen rows write the dump slot and stay) and embeds the new ``hist[pos]``."""
+        st = self.state
+        for g in st.groups:
+            b = self._forward_rows(g, 1)
+            ops.decode_finish(b.keys, g.nxt, g.hist, g.pos, st.s_mark, st.n_mark, self.w.embed, b.h, b.psq)
+        return st.nxt
+
+    def _issue_verify(self):
+        """One speculative verify step (``engine/engine.py:955-1003``): prompt-lookup drafts of k
+        tokens, one forward over T = k + 1 tokens per row, acceptance of the leading matches
+        (history scatter, position advance, next input row). Single row group (B <= 8)."""
+        st = self.state
+        g = st.groups[0]
+        T = st.k + 1
+        b = self.bufs(g, T)
+        ops.spec_draft(g.hist, g.pos, st.k, CONFIG["spec_n"], out=b.tok)
+        self._forward_rows(g, T, tok=b.tok)
+        b1 = self.bufs(g, 1)
+        ops.spec_accept(b.nxt, b.tok, g.hist, g.pos, st.s_mark, st.n_mark, self.w.embed, b1.h, b1.psq, b.out_t, b.adv)
+        return b.out_t, b.adv
+
+    def _plain(self):
+        st = self.state
+        if CONFIG["graphs"] and 1 in st.graphs:
+            return st.graphs[1].launch()
+        return self._issue_plain()
+
+    def _verify(self):
+        st = self.state
+        T = st.k + 1
+        if CONFIG["graphs"] and T in st.graphs:
+            return st.graphs[T].launch()
+        return self._issue_verify()
+
+    # ================================================================== certification
+    def certify(self, g: rt.RowGroup, T: int, seed: int = 0) -> dict:
         """Warmup certification (``engine/engine.py:407-486``) of the kernels one decode step of
-        ``(B, T)`` runs, on that step's own buffers, launch configurations and KV capacity.
+        row group ``g`` and width ``T`` runs, on that step's own buffers, launch shapes and KV
+        capacity.
 
         Layer 0 and the LM head run through ``_layer`` / ``_lm_head`` on a seeded N(0, 1) residual
         stream, with layer 0's cache prefix filled with N(0, 1) keys and values and ragged
-        positions (every slot of it is rewritten by the prompt forward or by a decode step before
-        any step reads it). Each stage is compared with its twin (``qwen_hip.twins``) fed the
-        kernels' own output of the stage before, so a mismatch names the stage; the standalone
-        operators of the reference's ``ops`` table are checked on the same data. The bars are the
-        reference's: ``atol 1e-2, rtol 1/64``, attention ``1e-2 / 1e-2``, the V-cache copy and
-        the residual stream of ``add_rms_norm`` bit-exact, and greedy tokens within two bf16 ulps
-        of the twin's maximum logit.
+        positions (the prompt forward or a decode step rewrites every slot of it before any step
+        reads it). Each stage is compared with its twin (``qwen_hip.twins``) fed the kernels' own
+        output of the stage before, so a mismatch names the stage; the operators of the
+        reference's ``ops`` table are checked on the same data. Bars: ``atol 1e-2, rtol 1/64``,
+        attention ``1e-2 / 1e-2``, the V copy and the residual of ``add_rms_norm`` bit-exact,
+        greedy tokens within two bf16 ulps of the twin's maximum logit.
 
-        Unlike the reference, a failed stage is not replaced by its twin (that would put a non-HIP
-        computation into the decode step): the engine raises ``RuntimeError`` and the shape stays
-        uncertified. Returns the verdict ``{stage: bool}`` (kept in ``self.certified[(B, T)]``).
-        """
-        M, dev, eps = B * T, self.device, self.eps
-        b = self._buffers(B, T)
-        w = self.layers[0]
-        g = torch.Generator(device=dev).manual_seed(seed)
+        Unlike the reference, a failing stage is not replaced by its twin (that would put a
+        non-HIP computation into the decode step): the engine raises ``RuntimeError`` and the
+        shape stays uncertified. Returns the verdict ``{stage: bool}``."""
+        st, s, dev, eps = self.state, self.spec, self.device, self.eps
+        b = self.bufs(g, T)
+        M, rows = b.M, g.n
+        w = self.w.layers[0]
+        gd = torch.Generator(device=dev).manual_seed(seed)
         gh = torch.Generator().manual_seed(seed)
-        pos = torch.randint(0, self.CAP - T, (B,), generator=gh, dtype=torch.int32)
+        pos = torch.randint(0, st.cap - T - 1, (rows,), generator=gh, dtype=torch.int32)
         pos_d = pos.to(dev)
         lengths = pos_d + T
-        kc, vc = self.k_cache[0], self.v_cache[0]
-        Lmax = int(pos.max()) + T
+        kc, vc = g.kv[0]
+        top = int(pos.max()) + T
         verdict = {}
 
         def check(name, ok):
             verdict[name] = verdict.get(name, True) and bool(ok)
 
+        saved_pos = g.pos.clone()
         with torch.inference_mode():
-            kc[:, :, :Lmax].normal_(generator=g)
-            vc[:, :, :Lmax].normal_(generator=g)
-            h0 = torch.randn((M, self.H), generator=g, device=dev).to(BF16)
-            self.pos_buf.copy_(pos_d)
-            b["h"].copy_(h0)
-            ops.sumsq16(b["h"], out=b["psq"])
+            kc[:, :, :top].normal_(generator=gd)
+            vc[:, :, :top].normal_(generator=gd)
+            h0 = torch.randn((M, s.H), generator=gd, device=dev).to(BF16)
+            g.pos.copy_(pos_d)
+            b.h.copy_(h0)
+            ops.sumsq16(b.h, out=b.psq)
             trace = []
-            self._layer(0, b, T, trace=trace)
-            self._lm_head(b, M, extract=True)
+            self._layer(0, g, b, trace=trace)
+            self._lm_head(b, extract=True)
             qkv_k, a_k, h1_k, p_k, h2_k = trace
-            nxt = b["next"].clone()
-            # decode-step stages, each twin fed the kernels' previous stage
-            check("step.norm_qkv", tw.close(qkv_k, tw.linear(tw.rms_norm(h0, w.ln1, eps), w.r_qkv)))
+            nxt = b.nxt.clone()
+            qkv_w = self.w.natural_qkv_rows(w)
+            check("step.norm_qkv", tw.close(qkv_k, tw.linear(tw.rms_norm(h0, w.ln1, eps), qkv_w)))
             q_t, k_t, v_t = tw.qk_norm_rope(qkv_k, w.q_norm, w.k_norm, eps, self.cos_tab, self.sin_tab, pos_d, T,
-                                            self.Nkv)
-            bi = torch.arange(B, device=dev)[:, None].expand(B, T)
+                                            s.Nkv)
+            bi = torch.arange(rows, device=dev)[:, None].expand(rows, T)
             slots = pos_d.to(torch.int64)[:, None] + torch.arange(T, device=dev)[None, :]
             check("step.kv_write", tw.close(kc.transpose(1, 2)[bi, slots], k_t)
                   and torch.equal(vc.transpose(1, 2)[bi, slots], v_t))
             a_t = tw.attention(q_t, kc, vc, lengths, self.scale)
             check("step.attention", tw.close(a_k, a_t, atol=1e-2, rtol=1e-2))
-            o_t = tw.linear(a_k.view(M, -1), w.r_o)
+            o_t = tw.linear(a_k.view(M, -1), w.o_rows)
             check("step.o_residual", tw.close(h1_k, tw.add(h0, o_t)))
-            gu_t = tw.linear(tw.rms_norm(h1_k, w.ln2, eps), w.r_gu)
+            gu_t = tw.linear(tw.rms_norm(h1_k, w.ln2, eps), w.gu_rows)
             check("step.norm_gate_up_swiglu", tw.close(p_k, tw.silu_mul(gu_t)))
-            check("step.down_residual", tw.close(h2_k, tw.add(h1_k, tw.linear(p_k, w.r_down))))
-            logits = tw.linear(tw.rms_norm(h2_k, self.final_norm, eps), self.embed_rows)
+            check("step.down_residual", tw.close(h2_k, tw.add(h1_k, tw.linear(p_k, w.down_rows))))
+            logits = tw.linear(tw.rms_norm(h2_k, self.w.final_norm, eps), self.w.lm_rows)
             check("step.norm_lm_head_argmax", tw.argmax_ok(nxt, logits))
-            # the reference's operator table on the same data
             for name, op in self.ops.items():
                 if name == "rms_norm":
                     check(name, tw.close(op(h0, w.ln1, eps), tw.rms_norm(h0, w.ln1, eps)))
@@ -560,326 +633,162 @@ class Engine:
                           and torch.equal(vc2.transpose(1, 2)[bi, slots], v_t))
                     del kc2, vc2
                 elif name == "attn_decode" and T <= 16:
-                    splits = ops.choose_num_splits(B, self.Nkv, self.CAP, T)
+                    splits = ops.choose_num_splits(rows, s.Nkv, st.cap, T)
                     a_o = op(q_t, kc, vc, lengths.to(torch.int32), self.scale, splits)
                     check(name, tw.close(a_o, a_t, atol=1e-2, rtol=1e-2))
+            g.pos.copy_(saved_pos)
         torch.cuda.synchronize()
-        _log(f"certified on B={B} T={T}: {verdict}")
+        _log(f"certified rows={rows} T={T}: {verdict}")
         failed = [k for k, ok in verdict.items() if not ok]
         if failed:
-            raise RuntimeError(f"kernel certification failed on B={B} T={T} for {failed}; "
+            raise RuntimeError(f"kernel certification failed on rows={rows} T={T} for {failed}; "
                                "the engine has no fallback path")
-        self.certified[(B, T)] = verdict
+        st.certified[(rows, T)] = verdict
         return verdict
 
-    def _plain_step(self):
-        """``_plain_step`` (``engine/engine.py:941-953``): step on hist[pos], write hist[pos+1], pos += 1,
-        and leave the embedding of the new hist[pos] in ``h`` for the next step."""
-        self._step(1)
-        b = self._buffers(self.B, 1)
-        ops.decode_finish(b["keys"], b["next"], self.hist_buf, self.pos_buf, self.s_buf, self.ntarget_buf, self.embed,
-                          b["h"], b["psq"])
-        return b["next"]
-
-    def _prime(self):
-        """Embed ``hist[b, pos[b]]`` into the plain step's input rows (before the first decode step)."""
-        b = self._buffers(self.B, 1)
-        ops.embed_hist(self.hist_buf, self.pos_buf, self.embed, b["h"], psq_out=b["psq"])
-
-    def _spec_step(self, k):
-        """``_spec_step`` (``engine/engine.py:979-1003``): draft ``k`` tokens per sequence by prompt
-        lookup, verify them in one T = k+1 step, accept the leading matches. Returns ``(out_t [T, B],
-        adv [B])``; also leaves the embedding of the new ``hist[pos]`` in the plain step's input rows."""
-        B, T = self.B, k + 1
-        b = self._buffers(B, T)
-        b1 = self._buffers(B, 1)
-        ops.spec_draft(self.hist_buf, self.pos_buf, k, CONFIG["spec_n"], out=b["tok"])
-        nxt = self._step(T, tok=b["tok"])
-        ops.spec_accept(nxt, b["tok"], self.hist_buf, self.pos_buf, self.s_buf, self.ntarget_buf, self.embed,
-                        b1["h"], b1["psq"], b["out_t"], b["adv"])
-        return b["out_t"], b["adv"]
-
-    def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
-        """Greedy next token at every position of ``tok [B, T]`` (the speculative verify forward
-        of ``engine/engine.py:979-993``): token ``t`` of row ``b`` sits at ``positions[b] + t``;
-        K/V are written for those slots. Returns ``[B, T]`` int64 (host sync)."""
-        B, T = tok.shape
-        assert B == self.B and B * T <= 32 and T <= 16, "verify needs the prepared batch, B*T <= 32, T <= 16"
-        with torch.inference_mode():
-            pos = torch.as_tensor(positions, dtype=torch.int32).reshape(B)
-            self.pos_buf.copy_(pos.to(self.device))
-            out = self._step(T, tok=tok.to(self.device, torch.int64).contiguous()).view(B, T).clone()
-        return out
-
-    def step_hidden(self, tok: torch.Tensor, positions) -> list:
-        """One eager decode step of ``tok [B, 1]`` at ``positions``; returns the residual stream
-        after every layer (for per-layer parity checks)."""
-        hidden = []
-        with torch.inference_mode():
-            self.pos_buf.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
-            self._step(1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
-        return [h.clone() for h in hidden]
-
-    @torch.inference_mode()
-    def _capture(self, T):
-        """Record one decode step into a HIP graph (``engine/engine.py:1005-1042``): the plain step
-        (T = 1) or the speculative verify step (T = k + 1).
-
-        Always under inference mode: the first capture in a process creates the generator state
-        that later captures update in place, so every capture must run in the same mode (the
-        engine's own callers capture inside ``generate``)."""
-        k = T - 1
-        run = self._plain_step if k == 0 else (lambda: self._spec_step(k))
-        pos_saved = self.pos_buf.clone()
-        hist_saved = self.hist_buf.clone()
-        s_saved, n_saved = self.s_buf.clone(), self.ntarget_buf.clone()
-        self.s_buf.zero_()
-        self.ntarget_buf.fill_(1 << 40)
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            self.pos_buf.fill_(1)
-            run()                           # warm-up (allocates nothing new)
-        torch.cuda.current_stream().wait_stream(stream)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        self.pos_buf.fill_(1)
-        with torch.cuda.graph(graph):
-            out = run()
-        torch.cuda.synchronize()
-        self.graphs[T] = (graph, out)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 5
-        start.record()
-        for _ in range(reps):
-            self.pos_buf.fill_(1)
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        self.step_ms[T] = start.elapsed_time(end) / reps
-        # Capture wrote K/V at slots 1..T and hist[:, 2..T+1]: the prompt forward and the
-        # first decode steps overwrite those slots before anything reads them.
-        self.pos_buf.copy_(pos_saved)
-        self.hist_buf.copy_(hist_saved)
-        self.s_buf.copy_(s_saved)
-        self.ntarget_buf.copy_(n_saved)
-        torch.cuda.synchronize()
-        _log(f"captured T={T} graph; replay {self.step_ms[T]:.3f} ms/step")
-
-    # ------------------------------------------------------------------ prompt forward
-    def _prefill_attention(self, q, kc, vc, S):
-        """Causal attention of the prompt: q ``[Bs, S, Nq, D]``, cache views -> ``[Bs*S, Nq*D]``.
-
-        Uses torch SDPA restricted to its flash / memory-efficient kernels; if
-        neither accepts the shape, the decode-attention kernel runs over
-        16-token chunks of the prompt (same causal rule).
-        """
-        Bs = q.shape[0]
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-        if self.sdpa_mode != "chunked":
-            try:
-                qt = q.transpose(1, 2)
-                rep = self.Nq // self.Nkv
-                k = kc[:, :, :S]
-                v = vc[:, :, :S]
-                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                    if self.sdpa_mode in (None, "gqa"):
-                        try:
-                            out = F.scaled_dot_product_attention(qt, k, v, is_causal=True, scale=self.scale,
-                                                                 enable_gqa=True)
-                            self.sdpa_mode = "gqa"
-                            return out.transpose(1, 2).reshape(Bs * S, self.Nq * self.D)
-                        except RuntimeError:
-                            self.sdpa_mode = "expand"
-                    ke = k[:, :, None].expand(Bs, self.Nkv, rep, S, self.D).reshape(Bs, self.Nq, S, self.D)
-                    ve = v[:, :, None].expand(Bs, self.Nkv, rep, S, self.D).reshape(Bs, self.Nq, S, self.D)
-                    out = F.scaled_dot_product_attention(qt, ke, ve, is_causal=True, scale=self.scale)
-                    return out.transpose(1, 2).reshape(Bs * S, self.Nq * self.D)
-            except RuntimeError as error:
-                _log(f"SDPA flash/efficient unavailable ({error!r}); chunked decode-attention kernel")
-                self.sdpa_mode = "chunked"
-        out = torch.empty((Bs, S, self.Nq * self.D), dtype=BF16, device=self.device)
-        lengths = torch.empty((Bs,), dtype=torch.int32, device=self.device)
-        for t0 in range(0, S, 16):
-            T = min(16, S - t0)
-            lengths.fill_(t0 + T)
-            splits = ops.choose_num_splits(Bs, self.Nkv, t0 + T)
-            out[:, t0:t0 + T] = ops.attn_decode(q[:, t0:t0 + T].contiguous(), kc, vc, lengths, self.scale, splits)
-        return out.reshape(Bs * S, self.Nq * self.D)
-
-    def _prefill(self, ids):
-        """Prompt forward (``engine/engine.py:1181-1189``): batch slices of at most prefill_rows rows."""
+    # ================================================================== prompt forward
+    def _prefill(self, ids: torch.Tensor, hidden=None) -> torch.Tensor:
+        """Prompt forward (``engine/engine.py:1181-1221``): fills the KV cache for positions
+        ``[0, S)`` of every sequence and returns the first greedy token per sequence (``[B]``
+        int64). The prompt runs in position chunks ``[p0, p1)`` of all ``B`` sequences
+        (``prefill_tokens`` rows each); a chunk's attention reads the keys of earlier chunks
+        from the cache. ``hidden`` (a list) receives the residual stream after each layer for
+        the positions of the last chunk, ``[B * (p1 - p0), H]`` (row ``b * (p1 - p0) + t``)."""
+        st, s, dev = self.state, self.spec, self.device
         B, S = ids.shape
-        rows_per = max(1, CONFIG["prefill_rows"] // S)
-        firsts = []
-        for b0 in range(0, B, rows_per):
-            b1 = min(B, b0 + rows_per)
-            firsts.append(self._prefill_slice(ids[b0:b1], b0))
-        return firsts[0] if len(firsts) == 1 else torch.cat(firsts)
+        chunk = max(1, min(S, CONFIG["prefill_tokens"] // B))
+        h = None
+        for p0 in range(0, S, chunk):
+            p1 = min(S, p0 + chunk)
+            Tc = p1 - p0
+            last = p1 == S
+            pos = torch.full((B,), p0, dtype=torch.int32, device=dev)
+            h = ops.embed(ids[:, p0:p1].reshape(-1).contiguous(), self.w.embed)
+            for l, w in enumerate(self.w.layers):
+                kc, vc = st.k(l), st.v(l)
+                n = ops.rms_norm(h, w.ln1, s.eps)
+                qkv = ops.gemm(n, w.qkv)
+                q = ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, pos, Tc,
+                                           kc, vc)
+                a = ops.attn_prefill(q, kc, vc, p0, self.scale)
+                ops.gemm(a.view(B * Tc, -1), w.o, residual=h, out=h)
+                n = ops.rms_norm(h, w.ln2, s.eps)
+                p = ops.gemm(n, w.gu, silu_pair=True)
+                ops.gemm(p, w.down, residual=h, out=h)
+                if hidden is not None and last:
+                    hidden.append(h.clone())
+        h_last = h.view(B, -1, s.H)[:, -1].contiguous()
+        first = torch.empty((B,), dtype=torch.int64, device=dev)
+        for r0 in range(0, B, 32):
+            r1 = min(B, r0 + 32)
+            ops.lm_head_argmax(h_last[r0:r1], self.w.final_norm, s.eps, self.w.lm, out=first[r0:r1])
+        return first
 
-    def _prefill_slice(self, ids, b0, hidden=None):
-        """``_prefill_slice`` (``engine/engine.py:1191-1221``) for rows ``b0 .. b0 + Bs``."""
-        Bs, S = ids.shape
-        b1 = b0 + Bs
-        pos = torch.zeros((Bs,), dtype=torch.int32, device=self.device)
-        h = ops.embed(ids.reshape(-1).contiguous(), self.embed)
-        d = None
-        for l, w in enumerate(self.layers):
-            kc = self.k_cache[l][b0:b1]
-            vc = self.v_cache[l][b0:b1]
-            if d is None:
-                n = ops.rms_norm(h, w.ln1, self.eps)
-            else:
-                h, n = ops.add_rms_norm(h, d, w.ln1, self.eps)
-            qkv = F.linear(n, w.r_qkv)
-            q = ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, self.eps, self.cos_tab, self.sin_tab, pos, S, kc, vc)
-            a = self._prefill_attention(q, kc, vc, S)
-            o = F.linear(a, w.r_o)
-            h, n = ops.add_rms_norm(h, o, w.ln2, self.eps)
-            d = F.linear(ops.silu_mul(F.linear(n, w.r_gu)), w.r_down)
-            if hidden is not None:
-                hidden.append(ops.add_rms_norm(h, d, w.ln1, self.eps)[0])
-        last = torch.arange(Bs, device=self.device) * S + (S - 1)
-        hl, _ = ops.add_rms_norm(h.index_select(0, last), d.index_select(0, last), self.final_norm, self.eps)
-        firsts = []
-        for r0 in range(0, Bs, 32):
-            firsts.append(ops.lm_head_argmax(hl[r0:r0 + 32].contiguous(), self.final_norm, self.eps, self.embed))
-        return firsts[0] if len(firsts) == 1 else torch.cat(firsts)
+    # ================================================================== generate
+    def _token_ids(self, input_ids) -> torch.Tensor:
+        B = len(input_ids)
+        if B == 0:
+            raise ValueError("input_ids holds no sequence")
+        S = len(input_ids[0])
+        if S == 0 or any(len(row) != S for row in input_ids):
+            raise ValueError("all prompts must be non-empty and of the same length")
+        ids = torch.tensor(input_ids, dtype=torch.int64)
+        if int(ids.min()) < 0 or int(ids.max()) >= self.spec.V:
+            raise ValueError(f"token ids must lie in [0, {self.spec.V})")
+        return ids
 
-    # ------------------------------------------------------------------ generate
+    def start(self, input_ids, max_new_tokens: int) -> torch.Tensor:
+        """Everything ``generate`` does before its first yield: batch state, prompt forward,
+        history and positions, the first decode step's input rows. Returns the first token of
+        every sequence (``[B]`` int64 on the device)."""
+        ids_cpu = self._token_ids(input_ids)
+        B, S = ids_cpu.shape
+        N = int(max_new_tokens)
+        with torch.inference_mode():
+            st = self.prepare(B, S, N)
+            ids = ids_cpu.to(self.device)
+            first = self._prefill(ids)
+            st.hist[:, :S].copy_(ids)
+            st.hist[:, S].copy_(first)
+            st.pos.fill_(S)
+            st.marks[0] = S
+            st.marks[1] = N
+            for g in st.groups:
+                b = self.bufs(g, 1)
+                ops.embed_hist(g.hist, g.pos, self.w.embed, b.h, psq_out=b.psq)
+        return first
+
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):
-        """Greedy continuation of every sequence, one step at a time (``engine/engine.py:1225-1250``).
-
-        Yields a list with one token id per sequence for each output step,
-        exactly ``max_new_tokens`` times. Never stops at end-of-sequence tokens.
-        """
-        B, S = len(input_ids), len(input_ids[0])
+        """Greedy continuation of every sequence (``engine/engine.py:1225-1250``): yields a list of
+        one token id per sequence per output position, exactly ``max_new_tokens`` times; never
+        stops at an end-of-sequence token."""
         N = int(max_new_tokens)
         if N <= 0:
             return
-        if any(len(row) != S for row in input_ids):
-            raise ValueError("all prompts must have the same length")
+        first = self.start(input_ids, N)
+        st = self.state
+        k = st.k
+        t_plain = st.graphs[1].ms if 1 in st.graphs else 1.0
+        t_verify = st.graphs[k + 1].ms if k and (k + 1) in st.graphs else 1.0
+        policy = rt.SpecPolicy(k, t_plain, t_verify, CONFIG["spec_backoff"], CONFIG["spec_probe_len"],
+                               CONFIG["spec_policy"])
+        pump = rt.TokenPump(st.B, N, first, CONFIG["inflight"], k, self._plain, self._verify, policy,
+                            self.counters)
+        yield from pump
+
+    # ================================================================== test / bench hooks
+    def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
+        """Greedy next token at every position of ``tok [B, T]`` (the verify forward of
+        ``engine/engine.py:979-993``): token ``t`` of row ``b`` sits at ``positions[b] + t`` and
+        its K/V are written there. Needs the prepared batch in one row group. Returns ``[B, T]``
+        int64 (synchronises)."""
+        B, T = tok.shape
+        st = self.state
+        assert st is not None and B == st.B and len(st.groups) == 1 and B * T <= 32 and T <= 16
+        g = st.groups[0]
         with torch.inference_mode():
-            first = self.start(input_ids, N)
-            yield from self._decode_loop(first, B, N)
+            g.pos.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(B).to(self.device))
+            b = self._forward_rows(g, T, tok=tok.to(self.device, torch.int64).contiguous())
+            out = b.nxt.view(B, T).clone()
+        torch.cuda.synchronize()
+        return out
 
-    def start(self, input_ids: list[list[int]], max_new_tokens: int) -> torch.Tensor:
-        """The part of ``generate`` before the first yield (``engine/engine.py:1225-1248``): per-shape
-        state, prompt forward, history and positions, the first decode step's input row. Returns the
-        first token of every sequence (``[B]`` int64 on the device)."""
-        B, S, N = len(input_ids), len(input_ids[0]), int(max_new_tokens)
-        ids_cpu = torch.tensor(input_ids, dtype=torch.int64)
-        if ids_cpu.numel() and (int(ids_cpu.min()) < 0 or int(ids_cpu.max()) >= self.V):
-            raise ValueError(f"token ids must lie in [0, {self.V})")
+    def step_hidden(self, tok: torch.Tensor, positions) -> list:
+        """One eager decode step of ``tok [B, 1]`` at ``positions`` (prepared batch, one row
+        group); returns the residual stream after every layer."""
+        st = self.state
+        g = st.groups[0]
+        hidden = []
         with torch.inference_mode():
-            self._prepare(B, S, N)
-            ids = ids_cpu.to(self.device)
-            first = self._prefill(ids)
-            self.hist_buf[:, :S].copy_(ids)
-            self.hist_buf[:, S].copy_(first)
-            self.pos_buf.fill_(S)
-            self.s_buf.fill_(S)
-            self.ntarget_buf.fill_(N)
-            self._prime()
-        return first
+            g.pos.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
+            self._forward_rows(g, 1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
+        torch.cuda.synchronize()
+        return hidden
 
-    def _decode_loop(self, first, B, N):
-        """Pipelined graph replays with async D2H copies into a pinned ring (``engine/engine.py:1254-1378``).
+    def layer_step(self, l: int, hidden: torch.Tensor, positions, T: int = 1) -> list:
+        """One decoder layer on a given residual stream ``hidden [B*T, H]`` at ``positions`` (the
+        single-layer case): returns ``_layer``'s trace (qkv, attention
+        output, h after O, SwiGLU product, h after down). Prepared batch, one row group."""
+        st = self.state
+        g = st.groups[0]
+        b = self.bufs(g, T)
+        assert hidden.shape == (b.M, self.spec.H)
+        trace = []
+        with torch.inference_mode():
+            g.pos.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
+            b.h.copy_(hidden.to(self.device, BF16))
+            ops.sumsq16(b.h, out=b.psq)
+            self._layer(l, g, b, trace=trace)
+        torch.cuda.synchronize()
+        return trace
 
-        At most ``pipeline_depth + 1`` steps are in flight, and no step is launched that could
-        not contribute a token (``:1332-1336``). With speculation on, the loop alternates between
-        verify steps and plain steps: it speculates while the accepted tokens per verify step
-        (moving average of the slowest unfinished row) times the plain step time beat the verify
-        step time, and otherwise runs plain steps, probing speculation again every so often
-        (``:1319-1372``).
-        """
-        depth = CONFIG["pipeline_depth"]
-        ring = len(self.pin_nxt)
-        stream = torch.cuda.current_stream()
-        k = self.k_active
-        T = k + 1
-        graphs = self.graphs
-
-        def launch(slot, mode):
-            if mode == "first":
-                self.pin_nxt[slot][0].copy_(first, non_blocking=True)
-            elif mode == "plain":
-                if 1 in graphs:
-                    graphs[1][0].replay()
-                    out = graphs[1][1]
-                else:
-                    out = self._plain_step()
-                self.decode_launches += 1
-                self.pin_nxt[slot][0].copy_(out, non_blocking=True)
-            else:
-                if T in graphs:
-                    graphs[T][0].replay()
-                    out_t, adv = graphs[T][1]
-                else:
-                    out_t, adv = self._spec_step(k)
-                self.decode_launches += 1
-                self.spec_launches += 1
-                self.pin_nxt[slot].copy_(out_t, non_blocking=True)
-                self.pin_adv[slot].copy_(adv, non_blocking=True)
-            self.events[slot].record(stream)
-
-        t1 = self.step_ms.get(1, 1.0)
-        tk = self.step_ms.get(T, 1.0) if k else float("inf")
-        mode = "spec" if k else "plain"
-        rate = tk / t1 + 0.25 if k else 0.0       # optimistic start: speculate first
-        plain_left = probe_left = 0
-        probe_plain, probe_spec = CONFIG["spec_probe"]
-        losing = lambda: rate * t1 < tk * 1.03   # noqa: E731
-
-        queues = [deque() for _ in range(B)]
-        produced = [0] * B
-        inflight = deque()
-        launch(0, "first")
-        inflight.append((0, "first"))
-        launched = 1
-        potential = 1      # upper bound on the tokens per sequence the in-flight steps can still bring
-        yielded = 0
-        while yielded < N:
-            while len(inflight) <= depth and min(produced) + potential < N:
-                slot = launched % ring
-                launched += 1
-                if k:
-                    if mode == "plain":
-                        plain_left -= 1
-                        if plain_left <= 0:
-                            mode, probe_left = "spec", probe_spec
-                    elif probe_left > 0:
-                        probe_left -= 1
-                        if probe_left == 0 and losing():
-                            mode, plain_left = "plain", probe_plain
-                m = mode
-                if m == "spec" and N - min(produced) - potential <= 1:
-                    m = "plain"    # one token left: the cheap step wins
-                launch(slot, m)
-                inflight.append((slot, m))
-                potential += T if m == "spec" else 1
-            slot, m = inflight.popleft()
-            potential -= T if m == "spec" else 1
-            self.events[slot].synchronize()
-            if m == "spec":
-                rows = self.pin_nxt[slot].tolist()          # rows[j][b]
-                adv = self.pin_adv[slot].tolist()
-                gains = []
-                for b in range(B):
-                    a = int(adv[b])
-                    queues[b].extend(int(rows[j][b]) for j in range(a))
-                    produced[b] += a
-                    if produced[b] < N:
-                        gains.append(a)
-                if gains:
-                    rate = 0.75 * rate + 0.25 * min(gains)
-                    self.spec_tokens += min(gains)
-                    if probe_left == 0 and mode == "spec" and losing():
-                        mode, plain_left = "plain", probe_plain
-            else:
-                for b, t in enumerate(self.pin_nxt[slot][0].tolist()):
-                    queues[b].append(int(t))
-                    produced[b] += 1
-            while yielded < N and all(queues):
-                yield [q.popleft() for q in queues]
-                yielded += 1
+    def prefill_hidden(self, input_ids, N: int = 1):
+        """Prompt forward of ``input_ids`` on a fresh batch state; returns ``(first [B], hidden)``
+        with the residual stream after each layer (positions of the last prompt chunk)."""
+        ids = self._token_ids(input_ids)
+        hidden = []
+        with torch.inference_mode():
+            self.prepare(ids.shape[0], ids.shape[1], N)
+            first = self._prefill(ids.to(self.device), hidden=hidden)
+        torch.cuda.synchronize()
+        return first, hidden

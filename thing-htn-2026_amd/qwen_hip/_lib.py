@@ -46,6 +46,8 @@ SIGNATURES = {
     "qwen_decode_finish": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _ll, _i, _p]),
     "qwen_spec_draft": (_i, [_p, _p, _i, _i, _i, _i, _p, _p]),
     "qwen_spec_accept": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _ll, _i, _p]),
+    "qwen_gemm": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _i, _p]),
+    "qwen_attn_prefill": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _p]),
     "qwen_tile_weight": (_i, [_p, _p, _ll, _i, _i, _p]),
     "qwen_init_weight": (_i, [_p, _ll, _i, _i, _i, _pi, _pi, _i, ctypes.c_ulonglong, _f, _p]),
 }

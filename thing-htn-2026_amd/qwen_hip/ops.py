@@ -497,6 +497,55 @@ def rect_config(M: int, N: int, K: int, silu_pair: bool = False, cus: int = 256,
     return best
 
 
+# ----------------------------------------------------------- prompt forward
+
+PF_BN, PF_BK = 128, 64   # qwen_gemm: N must be a multiple of PF_BN, K of PF_BK
+
+
+def gemm(x: torch.Tensor, w: TiledWeight, *, residual: torch.Tensor | None = None, silu_pair: bool = False,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x @ w.T`` for any number of rows over a tiled weight (the prompt forward's projections,
+    ``engine/engine.py:1191-1221``), fp32 accumulation and one rounding, with the fused epilogues of
+    ``gemm_fused.py:136-173``: ``residual`` -> ``bf16(residual + bf16(acc))`` (``out`` may be the
+    residual itself); ``silu_pair`` (pair-interleaved gate|up weight) -> the SwiGLU product
+    ``[M, N/2]``."""
+    _gpu(x, residual, out)
+    assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
+    M, K = x.shape
+    assert K == w.K and w.N % PF_BN == 0 and K % PF_BK == 0, f"gemm: x [{M}, {K}] vs weight [{w.N}, {w.K}]"
+    assert silu_pair == w.pair and not (silu_pair and residual is not None)
+    ncols = w.N // 2 if silu_pair else w.N
+    if residual is not None:
+        assert residual.shape == (M, ncols) and residual.dtype == BF16 and residual.is_contiguous()
+    if out is None:
+        out = torch.empty((M, ncols), dtype=BF16, device=x.device)
+    assert out.shape == (M, ncols) and out.dtype == BF16 and out.is_contiguous()
+    epi = EPI_SWIGLU if silu_pair else (EPI_RES if residual is not None else EPI_STORE)
+    _lib.call("qwen_gemm", x.data_ptr(), w.data.data_ptr(), out.data_ptr(), M, w.N, K, ncols, _nullable(residual),
+              epi, _stream())
+    return out
+
+
+def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p0: int, scale: float,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal attention of a prompt chunk: ``q [B, T, Nq, D]`` holds the (normed, rotated) queries
+    of positions ``p0 .. p0 + T - 1`` of every sequence, whose keys and values are already in the
+    caches ``[B, Nkv, CAP, D]``; query ``t`` sees slots ``[0, p0 + t]``. Returns
+    ``[B, T, Nq * D]`` bf16 (``engine/engine.py:1123-1179``)."""
+    _gpu(q, k_cache, v_cache, out)
+    B, T, Nq, D = q.shape
+    Bk, Nkv, CAP, Dk = k_cache.shape
+    assert Bk == B and Dk == D and v_cache.shape == k_cache.shape and Nq == 4 * Nkv and D == 128
+    assert q.dtype == BF16 and q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()
+    assert 0 <= p0 and p0 + T <= CAP
+    if out is None:
+        out = torch.empty((B, T, Nq * D), dtype=BF16, device=q.device)
+    assert out.shape == (B, T, Nq * D) and out.is_contiguous()
+    _lib.call("qwen_attn_prefill", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), B, T, Nq,
+              Nkv, D, CAP, int(p0), float(scale), _stream())
+    return out
+
+
 GEMV_MAX_M = 2   # rows handled by the balanced row-major GEMV (qwen_gemv)
 GEPI_STORE, GEPI_RES, GEPI_SWIGLU, GEPI_ARGMAX = 0, 1, 2, 3
 
