@@ -1,25 +1,33 @@
 """Decode throughput of the MI355X Qwen3-4B engine (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config default|c2|c3|c4|c5]
 
-c5 (speculative verify steps) reports verify steps/s instead of decoded tokens/s.
+BASELINE.json's metric is "decode tok/s at B=1 and B=32 (Qwen3-4B bf16); HBM GB/s as % of peak".
+The default run measures both halves in one invocation on random-init Qwen3-4B bf16 weights
+(seed 0), greedy decoding through the engine's own ``generate()``:
 
-Default workload is BASELINE.json's configs[1] ("c2"): Qwen3-4B, random-init
-bf16 weights (seed 0), batch 1, a 128-token uniform-random prompt, greedy
-decoding. The engine's own generate() runs the prompt forward (untimed) and
-W warm-up steps, then K decode steps are timed between two device
-synchronisations; ``value`` = decoded tokens / wall seconds over the steps
-launched inside that window. Inputs and weights are resident in HBM
-throughout; only token ids cross PCIe (8 bytes per sequence per step).
+* ``value`` (B = 1, configs[1] "c2": a 128-token uniform-random prompt, 256 decode steps);
+* ``b32`` (B = 32, configs[3] "c4": 8192-token prompts, 256 decode steps, ~37 GiB of KV cache).
 
-Extra fields: ``roofline`` for the dominant kernel (the fused
-RMSNorm + gate/up GEMM + SwiGLU, 44% of the bytes of a B=1 step), timed live
-with HIP events on the stream it is launched on, rotating over the 36 layers'
-weights so that nothing is served from the 256 MB Infinity Cache;
-``step_roofline`` for the whole step (algorithmic bytes of weights + visible
-KV per step over the measured step time); ``cpu_baseline``: the oracle's
-torch-CPU restatement of the same decode step on this host's cores, over a
-bounded sample (2 of the 36 layers + the LM head, scaled to 36 layers).
+Each is timed as follows. The batch state is built, certified and its step graph recorded
+first (untimed); the prompt forward gives ``ttft_s``; ``W`` warm-up steps run; then the
+decode steps launched between two device synchronisations are timed, so ``value`` = decoded
+tokens / wall seconds over exactly those steps. Weights and KV cache are resident in HBM; only
+token ids cross PCIe (8 bytes per sequence per step).
+
+``roofline`` is for the dominant kernel of the workload, timed live with HIP events on the
+stream it runs on: at B = 1 the fused RMSNorm + gate/up GEMV + SwiGLU (44 % of a step's bytes),
+rotating over the 36 layers' weights so nothing is served from the 256 MB Infinity Cache; at
+B = 32 the decode attention (its KV stream is 83 % of the bytes), over the 36 layers' caches.
+``step_roofline``: algorithmic bytes of a whole step (weights + visible KV) over the measured
+step time. ``b32.mfma``: MFMA utilisation of the four projections at M = 32 (2 M N K flops per
+launch over the measured launch time, against the 2.5 PFLOP/s bf16 dense peak); they are
+HBM-bound, so this is a secondary figure. ``cpu_baseline``: the oracle's torch-CPU decode step
+over all 36 layers on this host's cores, median of 3 runs (a bounded sample of the c2 decode).
+
+``--config c3|c4`` run one decode config; ``--config c5`` replays the speculative verify graph
+(B = 4, T = 5, context 4096) and reports verify steps/s. ``--profile-sample`` runs only the
+dominant kernel (and a copy of known size) for rocprofv3 counter runs.
 """
 
 from __future__ import annotations
@@ -27,6 +35,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import tempfile
 import time
@@ -35,7 +44,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "thing-htn-2026_amd"))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s
+HBM_PEAK = 8.0e12        # MI355X HBM3E, bytes/s
+MFMA_BF16_PEAK = 2.5e15  # MI355X dense bf16 matrix peak, flop/s
 CONFIGS = {
     # name: (B, prompt length, decode steps), BASELINE.json configs[1..4]
     "c2": (1, 128, 256),
@@ -50,6 +60,9 @@ QWEN3_4B = {
     "head_dim": 128, "rms_norm_eps": 1e-6, "rope_theta": 5000000.0, "rope_scaling": None,
     "tie_word_embeddings": True,
 }
+DATA = ("synthetic: random-init bf16 weights (counter-based generator, seed 0, std 0.02), "
+        "uniform-random prompt ids (torch seed 1)")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def weight_bytes(cfg) -> int:
@@ -65,47 +78,22 @@ def kv_bytes_per_token(cfg) -> int:
     return cfg["num_hidden_layers"] * 2 * cfg["num_key_value_heads"] * cfg["head_dim"] * 2
 
 
-def eng_pipeline_depth() -> int:
-    from engine import CONFIG
-    return CONFIG["inflight"]
-
-
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    p.add_argument("--config", default="default", choices=["default"] + sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-layers", type=int, default=2)
     p.add_argument("--profile-sample", action="store_true",
-                   help="run only the dominant kernel (rotating over the layers) and a plain 1 GiB device copy, "
-                        "for rocprofv3 --pmc traffic runs; prints one JSON line")
+                   help="run only the dominant kernel of --config (c2: gate/up GEMV, c4: attention) and a plain "
+                        "1 GiB device copy, for rocprofv3 --pmc traffic runs; prints one JSON line")
     return p.parse_args()
 
 
-def profile_sample(eng, torch, T=1):
-    """Dominant-kernel launches plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
-    avg_s, k_bytes, _ = time_dominant_kernel(eng, torch, reps_per_layer=1, T=T)
-    n = 1 << 29                                # 2^29 bf16 = 1 GiB read + 1 GiB written per copy
-    src = torch.ones(n, dtype=torch.bfloat16, device=eng.device)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    return {"dominant_kernel_avg_us": round(avg_s * 1e6, 2), "dominant_kernel_bytes": k_bytes,
-            "copy_bytes_each_way": 2 * n, "copies": 3}
-
-
-# Measured HBM traffic of the dominant kernel (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
-# scaled by the same counters' reading for a plain copy of known size); written by
-# hand from the committed summary under profiles/ for the workload it names.
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
-
-
 def measured_traffic(config: str, kernel: str):
-    """Bytes per launch of ``kernel`` at ``config`` from the committed PMC summary (None if absent
-    or measured for another kernel)."""
+    """HBM bytes per launch of ``kernel`` at ``config`` from the committed PMC summary
+    (``FETCH_SIZE`` + ``WRITE_SIZE`` scaled by a copy of known size), or None."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
@@ -117,51 +105,162 @@ def measured_traffic(config: str, kernel: str):
     return entry.get("bytes_per_launch")
 
 
-def time_dominant_kernel(eng, torch, reps_per_layer=3, T=1):
-    """Average duration of the fused norm + gate/up + SwiGLU GEMM at the bench's M = B * T.
-
-    Timed with HIP events on the stream the kernel is launched on, rotating over
-    the 36 layers' weights (3.6 GB) so that nothing is served from cache.
-    """
-    from qwen_hip import ops
-    B = eng.B
-    b = eng.bufs(eng.state.groups[0], T)
-    h, p, psq, cfg, ws = b.h, b.p, b.psq, b.cfg["gu"], b.gemm_ws
-    stream = torch.cuda.current_stream()
-    ops.sumsq16(h, out=psq)
-
-    def run(w):
-        if b.gemv:    # M <= 2: the balanced row-major GEMV the engine runs
-            ops.gemv(h, w.gu_rows, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, cfg=b.gemv_cfg["gu"])
-        else:
-            ops.fused_linear(h, w.gu, cfg, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=p, psq_in=psq,
-                             workspace=ws)
-
-    for w in eng.w.layers[:2]:
-        run(w)
-    torch.cuda.synchronize()
+def _events_time(torch, run, n_outer, stream):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     n = 0
-    for _ in range(reps_per_layer):
-        for w in eng.w.layers:
-            run(w)
-            n += 1
+    for _ in range(n_outer):
+        n += run()
     end.record(stream)
     end.synchronize()
-    avg_s = start.elapsed_time(end) / 1e3 / n
+    return start.elapsed_time(end) / 1e3 / n
+
+
+def time_gate_up(eng, torch, reps=3, T=1):
+    """Average launch time of the fused RMSNorm + gate/up + SwiGLU projection at M = B * T, rotating
+    over the 36 layers' weights (3.6 GB). Returns (seconds, algorithmic bytes, kernel name)."""
+    from qwen_hip import ops
+    b = eng.bufs(eng.state.groups[0], T)
+    ops.sumsq16(b.h, out=b.psq)
+
+    def one(w):
+        if b.gemv:
+            ops.gemv(b.h, w.gu_rows, norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=b.p, cfg=b.gemv_cfg["gu"])
+        else:
+            ops.fused_linear(b.h, w.gu, b.cfg["gu"], norm_w=w.ln2, eps=eng.eps, silu_pair=True, out=b.p,
+                             psq_in=b.psq, workspace=b.gemm_ws)
+
+    def sweep():
+        for w in eng.w.layers:
+            one(w)
+        return len(eng.w.layers)
+
+    sweep()
+    torch.cuda.synchronize()
+    avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
     w0 = eng.w.layers[0].gu
-    M = B * T
-    bytes_launch = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
+    M = b.M
+    nbytes = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
     name = ("gemv_kernel<%d, %d, true, 2>" % (M, b.gemv_cfg["gu"][1]) if b.gemv
-            else ops.gemm_kernel_name(M, cfg, True, ops.EPI_SWIGLU))
-    return avg_s, bytes_launch, name
+            else ops.gemm_kernel_name(M, b.cfg["gu"], True, ops.EPI_SWIGLU))
+    return avg, nbytes, name
+
+
+def time_attention(eng, torch, reps=2):
+    """Average launch time of the decode attention (QK-norm + RoPE + KV write + attention + merge)
+    over the 36 layers' caches at the batch's current positions. Algorithmic bytes: the visible
+    K and V rows (B x ctx x Nkv x D x 2 x 2 B) plus the q/k/v rows read and the output written."""
+    from qwen_hip import ops
+    st = eng.state
+    g = st.groups[0]
+    b = eng.bufs(g, 1)
+    s = eng.spec
+    ctx = [int(v) + 1 for v in st.pos.tolist()]
+
+    def sweep():
+        for l, w in enumerate(eng.w.layers):
+            kc, vc = g.kv[l]
+            ops.attn_decode_mfma(b.qkv, w.q_norm, w.k_norm, s.eps, eng.cos_tab, eng.sin_tab, g.pos, 1, kc, vc,
+                                 eng.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves,
+                                 kv_cached=st.kv_cached)
+        return len(eng.w.layers)
+
+    sweep()
+    torch.cuda.synchronize()
+    avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
+    nbytes = sum(c * s.Nkv * s.D * 2 * 2 for c in ctx) + b.M * (s.qkv_width + s.Nq * s.D) * 2
+    name = f"attn_mfma_kernel<1, {b.attn_waves}, {'true' if st.kv_cached else 'false'}>"
+    return avg, nbytes, name
+
+
+def mfma_utilisation(eng, torch, reps=2):
+    """Flops over time of the four projections at the batch's M (MFMA kernels), rotating over layers."""
+    from qwen_hip import ops
+    b = eng.bufs(eng.state.groups[0], 1)
+    s = eng.spec
+    M = b.M
+    ops.sumsq16(b.h, out=b.psq)
+    a = b.a.view(M, -1)
+    h2 = b.h.clone()
+    kinds = {
+        "qkv": (lambda w: ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=s.eps, out=b.qkv,
+                                           psq_in=b.psq, workspace=b.gemm_ws), s.qkv_width, s.H),
+        "o": (lambda w: ops.fused_linear(a, w.o, b.cfg["o"], residual=h2, out=h2, workspace=b.gemm_ws),
+              s.H, s.Nq * s.D),
+        "gate_up": (lambda w: ops.fused_linear(b.h, w.gu, b.cfg["gu"], norm_w=w.ln2, eps=s.eps, silu_pair=True,
+                                               out=b.p, psq_in=b.psq, workspace=b.gemm_ws), 2 * s.I, s.H),
+        "down": (lambda w: ops.fused_linear(b.p, w.down, b.cfg["down"], residual=h2, out=h2,
+                                            workspace=b.gemm_ws), s.H, s.I),
+    }
+    out = {}
+    total_flops = total_s = 0.0
+    for name, (fn, N, K) in kinds.items():
+        def sweep(fn=fn):
+            for w in eng.w.layers:
+                fn(w)
+            return len(eng.w.layers)
+        sweep()
+        torch.cuda.synchronize()
+        avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
+        flops = 2.0 * M * N * K
+        out[name] = {"avg_us": round(avg * 1e6, 2), "tflops": round(flops / avg / 1e12, 1),
+                     "frac": round(flops / avg / MFMA_BF16_PEAK, 4),
+                     "hbm_frac": round(N * K * 2 / avg / HBM_PEAK, 4)}
+        total_flops += flops
+        total_s += avg
+    out["all"] = {"tflops": round(total_flops / total_s / 1e12, 1),
+                  "frac": round(total_flops / total_s / MFMA_BF16_PEAK, 4),
+                  "peak_tflops": MFMA_BF16_PEAK / 1e12, "M": M}
+    return out
+
+
+def run_decode(eng, torch, cfg, B, S, N, K, W):
+    """One greedy generate() of N tokens for B prompts of S tokens; K decode steps timed after W."""
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
+    total = max(N, 1 + W + K)
+    with torch.inference_mode():
+        eng.prepare(B, S, total)          # batch state, certification, step graph: untimed
+    torch.cuda.synchronize()
+    gen = eng.generate(prompt, total)
+    t_pf = time.perf_counter()
+    next(gen)                              # prompt forward + first token
+    ttft = time.perf_counter() - t_pf
+    for _ in range(W):
+        next(gen)
+    torch.cuda.synchronize()
+    l0 = eng.counters["decode"]
+    t0 = time.perf_counter()
+    for _ in gen:
+        pass
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    steps = eng.counters["decode"] - l0
+    if steps <= 0:
+        sys.exit(f"bench.py: no decode step was launched inside the timed window (--steps {K})")
+    dt = t1 - t0
+    ms_step = dt / steps * 1e3
+    ctx_mid = S + 1 + W + steps / 2
+    step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
+    return {
+        "value": round(steps * B / dt, 2), "steps": steps, "ms_per_step": round(ms_step, 4), "ttft_s": round(ttft, 3),
+        "step_roofline": {"bytes_per_step": int(step_bytes),
+                          "achieved_GBps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
+                          "frac": round(step_bytes / (ms_step / 1e3) / HBM_PEAK, 4)},
+    }
+
+
+def roofline(avg, nbytes, name, config, what):
+    achieved = nbytes / avg
+    return {"bound": "hbm", "kernel": f"{name}: {what}", "achieved": round(achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": measured_traffic(config, name), "avg_us": round(avg * 1e6, 2), "bytes_per_launch": int(nbytes)}
 
 
 def bench_verify(eng, torch, cfg, B, S, K, W):
     """c5: K speculative verify steps (T = SPEC_T tokens per sequence: the last accepted token and
     SPEC_T - 1 prompt-lookup drafts, which on a uniform-random prompt are effectively random ids),
-    each one replay of the captured verify graph (draft, 36 layers over B*T rows with causal
+    each one replay of the recorded verify graph (draft, 36 layers over B*T rows with causal
     multi-query attention, argmax per position, acceptance). ``value`` = verify steps per second."""
     T = SPEC_T
     g = torch.Generator().manual_seed(1)
@@ -180,75 +279,56 @@ def bench_verify(eng, torch, cfg, B, S, K, W):
     dt = time.perf_counter() - t0
     ctx_mid = (pos0 + int(eng.state.pos[0])) / 2 + T
     step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
-    avg_s, k_bytes, k_name = time_dominant_kernel(eng, torch, T=T)
-    achieved = k_bytes / avg_s
+    avg, nbytes, name = time_gate_up(eng, torch, T=T)
     return {
         "metric": f"spec-verify steps/s at B={B}, T={T}, context {S} (Qwen3-4B bf16)",
         "value": round(K / dt, 2), "unit": "verify steps/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(dt / K * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: random-init bf16 weights (counter-based generator, seed 0, std 0.02), uniform-random "
-                "prompt ids (torch seed 1); drafts by prompt lookup (no repeats: effectively random ids)",
+        "dtype": "bf16", "data": DATA + "; drafts by prompt lookup (no repeats: effectively random ids)",
         "config": {"workload": f"c5: Qwen3-4B, B={B}, context {S}, T={T} verify steps",
                    "global_batch": B, "seq_len": S, "verify_tokens": T, "parallelism": "single GPU"},
         "positions_per_s": round(K * B * T / dt, 1),
-        "roofline": {"bound": "hbm", "kernel": f"{k_name}: RMSNorm + gate/up + SwiGLU (one layer)",
-                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic("c5", k_name),
-                     "avg_us": round(avg_s * 1e6, 2), "bytes_per_launch": k_bytes},
+        "roofline": roofline(avg, nbytes, name, "c5", "RMSNorm + gate/up + SwiGLU (one layer)"),
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "achieved_GBps": round(step_bytes * K / dt / 1e9, 1),
                           "frac": round(step_bytes * K / dt / HBM_PEAK, 4)},
     }
 
 
-def cpu_baseline(eng, cfg, B, S, layers):
-    """Time the oracle's torch-CPU decode step on a 2-layer slice of the same weights."""
+def cpu_baseline(eng, cfg, S, runs=3, target_s=6.0):
+    """The oracle's torch-CPU decode step (oracle/model.py, all 36 layers + LM head) on this host's
+    cores, B = 1 at context ~S: median over ``runs`` runs of about ``target_s`` seconds each."""
     import torch
     from oracle.model import CpuQwen3
-
-    lw = []
-    for w in eng.w.layers[:layers]:
-        lw.append({"ln1": w.ln1.cpu(), "ln2": w.ln2.cpu(), "q_norm": w.q_norm.cpu(), "k_norm": w.k_norm.cpu(),
-                   "w_qkv": eng.w.natural_qkv_rows(w).cpu(), "w_o": w.o_rows.cpu(), "w_gu": w.gu_rows.cpu(),
-                   "w_down": w.down_rows.cpu()})
-    weights = {"embed": eng.w.lm_rows.cpu(), "final_norm": eng.w.final_norm.cpu(), "layers": lw}
-    ref = CpuQwen3(dict(cfg, num_hidden_layers=layers), weights)
+    w = eng.w
+    layers = [{"ln1": lw.ln1.cpu(), "ln2": lw.ln2.cpu(), "q_norm": lw.q_norm.cpu(), "k_norm": lw.k_norm.cpu(),
+               "w_qkv": w.natural_qkv_rows(lw).cpu(), "w_o": lw.o_rows.cpu(), "w_gu": lw.gu_rows.cpu(),
+               "w_down": lw.down_rows.cpu()} for lw in w.layers]
+    ref = CpuQwen3(cfg, {"embed": w.lm_rows.cpu(), "final_norm": w.final_norm.cpu(), "layers": layers})
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    max_steps = 64
-    ref.prepare(B, ((S + max_steps + 64) // 64) * 64)
     g = torch.Generator().manual_seed(1)
-    ids = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    ids = torch.randint(0, cfg["vocab_size"], (1, S), generator=g)
+    rates = []
     with torch.inference_mode():
-        # The S context slots get seeded random K/V in place of the prompt forward: a decode
-        # step's work does not depend on the cached values, and the oracle's prefill would hold
-        # [B, heads, S, S] fp32 scores (275 GB at B = 32, S = 8192).
+        ref.prepare(1, ((S + 256 + 63) // 64) * 64)
+        # the S context slots hold seeded random K/V in place of the prompt forward (a decode
+        # step's work does not depend on the cached values)
         for kc, vc in zip(ref.k_cache, ref.v_cache):
             kc[:, :, :S].copy_(torch.randn(kc[:, :, :S].shape, generator=g).to(kc.dtype))
             vc[:, :, :S].copy_(torch.randn(vc[:, :, :S].shape, generator=g).to(vc.dtype))
         ref.hist[:, :S] = ids
         ref.pos.fill_(S - 1)
-        ref.plain_step()                       # warm-up
-        t_layers, t_head, steps = 0.0, 0.0, 0
-        t_end = time.perf_counter() + 15.0
-        while (time.perf_counter() < t_end or steps < 2) and steps < max_steps:
-            tok = ref.hist.gather(1, ref.pos.to(torch.int64)[:, None])
+        t0 = time.perf_counter()
+        ref.plain_step()                   # warm-up, and the per-step estimate
+        per = time.perf_counter() - t0
+        n = max(2, min(60, int(target_s / max(per, 1e-3))))
+        for _ in range(runs):
+            ref.pos.fill_(S - 1)
             t0 = time.perf_counter()
-            h = ref.w["embed"][tok.reshape(-1)]
-            d = None
-            for l in range(layers):
-                h, d = ref.layer(l, h, d, ref.pos, 1, B)
-            t1 = time.perf_counter()
-            from oracle import ref_torch as R
-            _, n = R.add_rms_norm(h, d, ref.w["final_norm"], ref.eps)
-            R.argmax_lowest(R.linear(n, ref.w["embed"]))
-            t2 = time.perf_counter()
-            ref.pos += 1
-            t_layers += t1 - t0
-            t_head += t2 - t1
-            steps += 1
-    per_token = (t_layers / steps) * cfg["num_hidden_layers"] / layers + t_head / steps
+            for _ in range(n):
+                ref.plain_step()
+            rates.append(n / (time.perf_counter() - t0))
     cpu = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -258,90 +338,102 @@ def cpu_baseline(eng, cfg, B, S, layers):
                     break
     except OSError:
         pass
-    return {"value": round(B / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle torch-CPU decode step (oracle/model.py) on {layers} of "
-                       f"{cfg['num_hidden_layers']} layers + LM head, {steps} steps at context ~{S} (B={B}, "
-                       f"random cached K/V), scaled to {cfg['num_hidden_layers']} layers; host CPU {cpu}")}
+    return {"value": round(statistics.median(rates), 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "runs": [round(r, 3) for r in rates],
+            "sample": (f"oracle torch-CPU decode step (oracle/model.py), all {cfg['num_hidden_layers']} layers + LM "
+                       f"head, B=1 at context {S}..{S + n} (random cached K/V), {n} steps per run, median of "
+                       f"{runs} runs; host CPU {cpu}")}
+
+
+def profile_sample(eng, torch, config):
+    """Dominant-kernel launches plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
+    if config == "c4":
+        avg, nbytes, name = time_attention(eng, torch, reps=1)
+    else:
+        avg, nbytes, name = time_gate_up(eng, torch, reps=1, T=SPEC_T if config == "c5" else 1)
+    n = 1 << 29                                # 2^29 bf16 = 1 GiB read + 1 GiB written per copy
+    src = torch.ones(n, dtype=torch.bfloat16, device=eng.device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"kernel": name, "avg_us": round(avg * 1e6, 2), "bytes_per_launch": nbytes,
+            "copy_bytes_each_way": 2 * n, "copies": 3}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build runs on a single MI355X); got --gpus {args.gpus}",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only (every box in this build has a single MI355X; sequences "
+              f"would shard data-parallel, see DESIGN.md); got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
     import torch
+    import engine as engine_mod
     from __graft_entry__ import write_random_model
     from engine import Engine
 
-    B, S, N = CONFIGS[args.config]
-    K = args.steps if args.steps is not None else N
-    W = args.warmup
     cfg = QWEN3_4B
+    W = args.warmup
     if args.config == "c5":
-        import engine as engine_mod
         engine_mod.CONFIG["spec_k"] = SPEC_T - 1
     with tempfile.TemporaryDirectory() as d:
         eng = Engine(write_random_model(d, cfg, seed=0, std=0.02))
-    if args.config == "c5" and not args.profile_sample:
+
+    if args.profile_sample:
+        name = "c2" if args.config == "default" else args.config
+        B, S, N = CONFIGS[name]
+        engine_mod.CONFIG["certify"] = False
+        if name == "c4":
+            eng.start(torch.randint(0, cfg["vocab_size"], (B, S)).tolist(), 8)
+        else:
+            with torch.inference_mode():
+                eng.prepare(B, S, N + W + 1)
+        print(json.dumps(profile_sample(eng, torch, name)), flush=True)
+        return
+    if args.config == "c5":
+        B, S, N = CONFIGS["c5"]
+        K = args.steps if args.steps is not None else N
         print(json.dumps(bench_verify(eng, torch, cfg, B, S, K, W)), flush=True)
         return
-    if args.profile_sample:
-        # counter calibration only: the warmup certification's KV-sized copies would sit next to
-        # the calibration copy in the counter log
-        import engine as engine_mod
-        engine_mod.CONFIG["certify"] = False
-        eng.prepare(B, S, K + W + 1)
-        print(json.dumps(profile_sample(eng, torch, T=SPEC_T if args.config == "c5" else 1)), flush=True)
-        return
-    g = torch.Generator().manual_seed(1)
-    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
-    total = 1 + W + K
-    gen = eng.generate(prompt, total)
-    t_pf = time.perf_counter()
-    next(gen)                                  # prompt forward + first token
-    ttft = time.perf_counter() - t_pf
-    for _ in range(W):
-        next(gen)
-    torch.cuda.synchronize()
-    l0 = eng.counters["decode"]
-    t0 = time.perf_counter()
-    for _ in gen:
-        pass
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    steps = eng.counters["decode"] - l0
-    if steps <= 0:
-        sys.exit(f"bench.py: no decode step was launched inside the timed window (--steps {K} is within the "
-                 f"engine's {eng_pipeline_depth()} steps of pipelining); use more steps")
-    dt = t1 - t0
-    tok_s = steps * B / dt
-    ms_step = dt / steps * 1e3
 
-    ctx_mid = S + 1 + W + steps / 2
-    step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
-    avg_s, k_bytes, k_name = time_dominant_kernel(eng, torch)
-    achieved = k_bytes / avg_s
+    first = "c2" if args.config == "default" else args.config
+    B, S, N = CONFIGS[first]
+    K = args.steps if args.steps is not None else N - 1 - W
+    res = run_decode(eng, torch, cfg, B, S, N, K, W)
+    avg, nbytes, name = time_gate_up(eng, torch)
     out = {
-        "metric": "decode tok/s at B=1 (Qwen3-4B bf16)" if B == 1 else f"decode tok/s at B={B} (Qwen3-4B bf16)",
-        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": W,
-        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: random-init bf16 weights (counter-based generator, seed 0, std 0.02), "
-                "uniform-random prompt ids (torch seed 1)",
-        "config": {"workload": f"{args.config}: Qwen3-4B, B={B}, prompt {S}, {N} greedy decode steps",
+        "metric": ("decode tok/s at B=1 and B=32 (Qwen3-4B bf16); HBM GB/s as % of peak" if args.config == "default"
+                   else f"decode tok/s at B={B} (Qwen3-4B bf16)"),
+        "value": res["value"], "unit": "tok/s", "n_gpus": 1, "steps": res["steps"], "warmup": W,
+        "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": DATA,
+        "config": {"workload": f"{first}: Qwen3-4B, B={B}, prompt {S}, {N} greedy decode steps",
                    "global_batch": B, "seq_len": S, "decode_steps": N, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": f"{k_name}: RMSNorm + gate/up + SwiGLU (one layer)",
-                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic(args.config, k_name),
-                     "avg_us": round(avg_s * 1e6, 2), "bytes_per_launch": k_bytes},
-        "step_roofline": {"bytes_per_step": int(step_bytes), "achieved_GBps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
-                          "frac": round(step_bytes / (ms_step / 1e3) / HBM_PEAK, 4)},
-        "ttft_s": round(ttft, 3),
+        "roofline": roofline(avg, nbytes, name, first, "RMSNorm + gate/up + SwiGLU (one layer)"),
+        "step_roofline": res["step_roofline"],
+        "ttft_s": res["ttft_s"],
+        "steps_note": ("steps = decode steps launched inside the timed window; the engine queues up to "
+                       f"{engine_mod.CONFIG['inflight']} steps ahead, so those launched before it are not counted"),
     }
+    if args.config == "default":
+        B4, S4, N4 = CONFIGS["c4"]
+        K4 = args.steps if args.steps is not None else N4 - 1 - W
+        r4 = run_decode(eng, torch, cfg, B4, S4, N4, K4, W)
+        a_avg, a_bytes, a_name = time_attention(eng, torch)
+        out["b32"] = {
+            "metric": "decode tok/s at B=32 (Qwen3-4B bf16)", "value": r4["value"], "unit": "tok/s",
+            "steps": r4["steps"], "ms_per_step": r4["ms_per_step"], "ttft_s": r4["ttft_s"],
+            "config": {"workload": f"c4: Qwen3-4B, B={B4}, prompts {S4}, {N4} greedy decode steps",
+                       "global_batch": B4, "seq_len": S4, "decode_steps": N4},
+            "roofline": roofline(a_avg, a_bytes, a_name, "c4",
+                                 "QK-norm + RoPE + KV write + GQA attention (one layer)"),
+            "step_roofline": r4["step_roofline"],
+            "mfma": mfma_utilisation(eng, torch),
+            "vs_b1": round(r4["value"] / res["value"], 3),
+        }
     if not args.no_cpu_baseline:
         try:
-            out["cpu_baseline"] = cpu_baseline(eng, cfg, B, S, args.cpu_layers)
+            out["cpu_baseline"] = cpu_baseline(eng, cfg, CONFIGS["c2"][1])
         except Exception as error:  # noqa: BLE001 - report, do not fail the GPU number
             out["cpu_baseline"] = {"value": None, "error": repr(error)[:200]}
     print(json.dumps(out), flush=True)

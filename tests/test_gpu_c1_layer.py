@@ -50,8 +50,9 @@ def test_c1_single_layer_per_tensor(c1, seed):
     k_pre = torch.randn(kv_shape, generator=g).to(BF16)
     v_pre = torch.randn(kv_shape, generator=g).to(BF16)
     hidden = torch.randn(1, cfg["hidden_size"], generator=g).to(BF16)
-    eng.state.k(0)[:, :, :CTX].copy_(k_pre.to(eng.device))
-    eng.state.v(0)[:, :, :CTX].copy_(v_pre.to(eng.device))
+    with torch.inference_mode():       # the engine's state tensors are inference tensors
+        eng.state.kcache(0)[:, :, :CTX].copy_(k_pre.to(eng.device))
+        eng.state.vcache(0)[:, :, :CTX].copy_(v_pre.to(eng.device))
     got_qkv, got_a, got_h1, got_p, got_h2 = [t.cpu() for t in eng.layer_step(0, hidden, [CTX])]
 
     # Oracle restatement of the layer (same weights, same cache contents).
@@ -74,7 +75,7 @@ def test_c1_single_layer_per_tensor(c1, seed):
     assert _rel(got_p, p) <= 2e-2, f"SwiGLU product: {_rel(got_p, p)}"
     assert _rel(got_h2, h2) <= 2e-2, f"layer output: {_rel(got_h2, h2)}"
     # The step's cache writes: slot CTX holds the normed, rotated key and the raw value.
-    kc, vc = eng.state.k(0)[0, :, CTX].cpu(), eng.state.v(0)[0, :, CTX].cpu()
+    kc, vc = eng.state.kcache(0)[0, :, CTX].cpu(), eng.state.vcache(0)[0, :, CTX].cpu()
     assert_close(kc, ref.k_cache[0][0, :, CTX], 1e-2, 1 / 64, "k slot")
     assert torch.equal(vc, ref.v_cache[0][0, :, CTX])
-    assert torch.equal(eng.state.k(0)[:, :, :CTX].cpu(), k_pre)   # prefilled slots untouched
+    assert torch.equal(eng.state.kcache(0)[:, :, :CTX].cpu(), k_pre)   # prefilled slots untouched

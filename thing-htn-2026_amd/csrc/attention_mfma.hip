@@ -160,16 +160,17 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const int wb0 = sb0 + wave, wb1 = sb1;  // this wavefront: blocks wb0, wb0 + BSTEP, .. < wb1
   const bool takes_new = split == p.S - 1 && wave == WPG - 1;
 
-  // Loads of one cached block (keys past nold re-read key 0, a valid slot, and are masked).
-  // A cached block's K (B operand: lane (q, r) holds key 16 nt + r, dims 32 kt + 8 q ..)
+  // Loads of one cached block: K (B operand: lane (q, r) holds key 16 nt + r, dims 32 kt + 8 q ..)
   // and V rows (lane (q, r) holds key 4 i + q, dims 8 r ..), read with non-temporal loads
   // (each cached byte is read once per step; measured on MI355X: 7.0 vs 6.2 TB/s for a
-  // plain streaming read). Keys past nold re-read slot 0, a valid row shared by all lanes,
-  // and are masked: a prefetch past the context costs no HBM traffic.
+  // plain streaming read). Keys past the split's range are masked.
   struct KVBlock {
     mu32x4 k[2][4], v[8];
   };
-  const int kend = nold;
+  // Keys at or past this split's range re-read slot 0 (a valid row every lane shares): a
+  // wavefront's unconditional first load and its prefetches past its last block then cost no
+  // HBM traffic and never touch a neighbouring split's blocks.
+  const int kend = min(nold, sb1 * MKB);
   auto load_block = [&](KVBlock& d, int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {

@@ -39,7 +39,7 @@ class BatchState:
     """Device state of one batch geometry ``(B, cap, k)``.
 
     * ``arena``: every layer's K and V cache in one allocation ``[L, 2, B, Nkv, cap, D]`` bf16;
-      ``k(l)`` / ``v(l)`` are the ``[B, Nkv, cap, D]`` views the kernels take (the reference's
+      ``kcache(l)`` / ``vcache(l)`` are the ``[B, Nkv, cap, D]`` views the kernels take (the reference's
       per-layer cache layout).
     * ``hist [B, cap]`` int64: prompt and emitted tokens; slot ``cap - 1`` is the dump slot that
       frozen rows write to.
@@ -65,10 +65,10 @@ class BatchState:
         self.certified = {}   # (rows, T) -> verdict
         self.kv_cached = False
 
-    def k(self, l):
+    def kcache(self, l):
         return self.arena[l, 0]
 
-    def v(self, l):
+    def vcache(self, l):
         return self.arena[l, 1]
 
     @property

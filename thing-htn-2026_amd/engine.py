@@ -411,10 +411,13 @@ class Engine:
         ok = 0 < k <= 15 and B <= CONFIG["spec_max_batch"] and B * (k + 1) <= 32
         return k if ok else 0
 
+    @torch.inference_mode()
     def prepare(self, B: int, S: int, N: int) -> rt.BatchState:
         """Batch state for ``B`` prompts of ``S`` tokens and ``N`` outputs: reused when the batch
         size and draft length match and its capacity suffices, else rebuilt. Certifies and
-        records the decode steps of the shape (once per state)."""
+        records the decode steps of the shape (once per state). Runs under inference mode: the
+        first graph recording in a process creates generator state that later recordings update
+        in place, so all of them must run in the same mode."""
         k = self._spec_k_for(B)
         cap = rt.capacity(S, N, k, CONFIG["cap_round"])
         self._rope_for(cap)
@@ -665,7 +668,7 @@ class Engine:
             pos = torch.full((B,), p0, dtype=torch.int32, device=dev)
             h = ops.embed(ids[:, p0:p1].reshape(-1).contiguous(), self.w.embed)
             for l, w in enumerate(self.w.layers):
-                kc, vc = st.k(l), st.v(l)
+                kc, vc = st.kcache(l), st.vcache(l)
                 n = ops.rms_norm(h, w.ln1, s.eps)
                 qkv = ops.gemm(n, w.qkv)
                 q = ops.qk_norm_rope_cache(qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, pos, Tc,
