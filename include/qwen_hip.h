@@ -8,7 +8,8 @@
  *   - Every entry point enqueues work on `stream` and returns immediately; it
  *     never allocates, frees or synchronises, so it can be recorded into a
  *     HIP graph. Return value: 0 on success, 1001 (bad size/shape argument),
- *     1002 (null pointer), 1003 (workspace too small), otherwise the
+ *     1002 (null pointer), 1003 (workspace too small), 1004 (request larger
+ *     than an allocation-free entry point's fixed scratch), otherwise the
  *     hipError_t of the failed launch.
  *   - "Tiled" weights use the MFMA-B tile layout written by
  *     qwen_tile_weight / qwen_init_weight: tile (nt, kt) of 16 rows x 32
@@ -102,6 +103,23 @@ int qwen_attn_decode_mfma_ex(const void* qkv, const void* q_norm_w, const void* 
                              void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
                              int CAP, int P, float eps, float scale, int num_splits, int waves, int flags,
                              hipStream_t stream);
+
+/* Fixed scratch of qwen_attn_decode_mfma_noalloc, per GPU (bytes). */
+#define QWEN_ATTN_NOALLOC_SCRATCH_BYTES (8LL << 20)
+
+/* qwen_attn_decode_mfma_ex without the workspace arguments: the split partials and arrival
+ * counters live in a fixed device array of QWEN_ATTN_NOALLOC_SCRATCH_BYTES per GPU (held until
+ * the process ends), so the call allocates nothing: no hipMalloc, hipFree or allocating library
+ * routine, and its counters are cleared by a kernel (not hipMemsetAsync), so it may be recorded
+ * into a HIP graph. A launch whose qwen_attn_mfma_workspace_bytes(B, T, Nkv, num_splits) exceeds
+ * that size returns 1004 and launches nothing. Every call on one GPU shares its array: calls that
+ * overlap on one GPU (on different streams) race. No counterpart in the reference; it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). */
+int qwen_attn_decode_mfma_noalloc(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                                  const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache,
+                                  void* out, int B, int T, int Nq, int Nkv, int D, int CAP, int P, float eps,
+                                  float scale, int num_splits, int waves, int flags, hipStream_t stream);
 
 /* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
  * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed

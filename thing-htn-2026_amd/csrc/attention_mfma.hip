@@ -27,6 +27,7 @@
 // workgroup reads a cache slot this launch writes.
 #include "common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -591,6 +592,41 @@ int launch_mfma(const MfmaAttnParams& p, int B, int waves, hipStream_t stream) {
   QWEN_RETURN_LAUNCH();
 }
 
+// ---- the allocation-free variant's scratch: one array per GPU, for the split partials and
+// arrival counters that qwen_attn_decode_mfma keeps in its caller's workspace. Host code never
+// passes `scratch` itself to a kernel (in host code it names a host-side stand-in); it looks up
+// each device's address once with hipGetSymbolAddress and uses that.
+constexpr long long NOALLOC_SCRATCH_BYTES = 8ll << 20;   // QWEN_ATTN_NOALLOC_SCRATCH_BYTES
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's address of `scratch` (looked up on its first use there), or null.
+void* device_scratch(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) { *status = (int)e; return nullptr; }
+  if (dev < 0 || dev >= MAX_DEVICES) { *status = QWEN_EARG; return nullptr; }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) { *status = e != hipSuccess ? (int)e : QWEN_ENULL; return nullptr; }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *status = QWEN_OK;
+  return g_scratch_ptr[dev];
+}
+
+// Zero `n` 32-bit words (the arrival counters) with a kernel rather than hipMemsetAsync, so a
+// caller may record the call into a HIP graph.
+__global__ void __launch_bounds__(256) zero_words_kernel(unsigned* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
 }  // namespace
 
 extern "C" {
@@ -633,6 +669,31 @@ int qwen_attn_decode_mfma_ex(const void* qkv, const void* q_norm_w, const void* 
   p.scale = scale; p.eps = eps;
   p.kv_cached = (flags & QWEN_ATTN_KV_CACHED) ? 1 : 0;
   return T <= 4 ? launch_mfma<1>(p, B, waves, stream) : launch_mfma<2>(p, B, waves, stream);
+}
+
+int qwen_attn_decode_mfma_noalloc(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                  const void* cos_tab, const void* sin_tab, const int32_t* positions, void* k_cache,
+                                  void* v_cache, void* out, int B, int T, int Nq, int Nkv, int D, int CAP, int P,
+                                  float eps, float scale, int num_splits, int waves, int flags, hipStream_t stream) {
+  if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || num_splits < 1 || num_splits > MERGE_MAX)
+    return QWEN_EARG;
+  const long long need = qwen_attn_mfma_workspace_bytes(B, T, Nkv, num_splits);
+  if (need > NOALLOC_SCRATCH_BYTES) return QWEN_ESCRATCH;
+  if (need == 0 || B == 0)
+    return qwen_attn_decode_mfma_ex(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out,
+                                    nullptr, 0, B, T, Nq, Nkv, D, CAP, P, eps, scale, num_splits, waves, flags,
+                                    stream);
+  int status = QWEN_OK;
+  void* ptr = device_scratch(&status);
+  if (!ptr) return status;
+  // the counters must start at zero (every launch re-arms them; cleared here all the same)
+  const int words = (int)(mfma_counter_bytes((long long)B * Nkv) / 4);
+  zero_words_kernel<<<(words + 255) / 256, 256, 0, stream>>>((unsigned*)ptr, words);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  return qwen_attn_decode_mfma_ex(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out, ptr,
+                                  NOALLOC_SCRATCH_BYTES, B, T, Nq, Nkv, D, CAP, P, eps, scale, num_splits, waves,
+                                  flags, stream);
 }
 
 int qwen_attn_decode_mfma(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,

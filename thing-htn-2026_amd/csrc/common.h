@@ -22,7 +22,8 @@ enum {
   QWEN_OK = 0,
   QWEN_EARG = 1001,      // a size / shape argument is out of the supported range
   QWEN_ENULL = 1002,     // a required pointer is null
-  QWEN_EWORKSPACE = 1003 // caller-provided workspace is too small
+  QWEN_EWORKSPACE = 1003, // caller-provided workspace is too small
+  QWEN_ESCRATCH = 1004    // the request needs more than an allocation-free entry point's fixed scratch
 };
 
 __device__ __forceinline__ float bf2f(bf16_t v) {

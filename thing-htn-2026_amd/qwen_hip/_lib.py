@@ -33,6 +33,8 @@ SIGNATURES = {
                                    _f, _i, _i, _p]),
     "qwen_attn_decode_mfma_ex": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _ll, _i, _i, _i, _i, _i, _i, _i,
                                       _f, _f, _i, _i, _i, _p]),
+    "qwen_attn_decode_mfma_noalloc": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _f,
+                                           _i, _i, _i, _p]),
     "qwen_sumsq16": (_i, [_p, _p, _i, _i, _p]),
     "qwen_linear_workspace_bytes": (_ll, [_i, _i, _i, _i]),
     "qwen_linear": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _i, _p, _ll, _p]),
@@ -52,7 +54,8 @@ SIGNATURES = {
     "qwen_init_weight": (_i, [_p, _ll, _i, _i, _i, _pi, _pi, _i, ctypes.c_ulonglong, _f, _p]),
 }
 
-_STATUS = {1001: "bad size/shape argument", 1002: "null pointer", 1003: "workspace too small"}
+_STATUS = {1001: "bad size/shape argument", 1002: "null pointer", 1003: "workspace too small",
+           1004: "request exceeds the allocation-free entry point's fixed scratch"}
 
 _lib = None
 

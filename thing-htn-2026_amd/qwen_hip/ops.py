@@ -266,6 +266,29 @@ def attn_decode_mfma(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, 
     return o
 
 
+ATTN_NOALLOC_SCRATCH_BYTES = 8 << 20   # qwen_attn_decode_mfma_noalloc's fixed scratch per GPU
+
+
+def attn_decode_mfma_noalloc(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, T, k_cache, v_cache, scale,
+                             num_splits, *, out: torch.Tensor, waves: int = 4, kv_cached: bool = False) -> torch.Tensor:
+    """``attn_decode_mfma`` through the allocation-free entry point: the split partials live in
+    the library's fixed per-GPU scratch (``ATTN_NOALLOC_SCRATCH_BYTES``), ``out`` is the caller's.
+    Raises ``RuntimeError`` (status 1004) when the shape needs more scratch than that."""
+    _gpu(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out)
+    B, Nkv, CAP, D = k_cache.shape
+    M, W = qkv.shape
+    Nq = W // D - 2 * Nkv
+    assert M == B * T and qkv.dtype == BF16 and qkv.is_contiguous() and k_cache.is_contiguous()
+    assert v_cache.is_contiguous() and v_cache.shape == k_cache.shape and positions.dtype == torch.int32
+    assert cos_tab.shape == sin_tab.shape and cos_tab.is_contiguous() and sin_tab.is_contiguous()
+    assert out.is_contiguous() and out.numel() == B * T * Nq * D and out.dtype == BF16
+    _lib.call("qwen_attn_decode_mfma_noalloc", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+              cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              out.data_ptr(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0], float(eps), float(scale), int(num_splits),
+              int(waves), ATTN_KV_CACHED if kv_cached else 0, _stream())
+    return out
+
+
 # ------------------------------------------------------- weights + GEMMs
 
 class TiledWeight:
