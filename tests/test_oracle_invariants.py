@@ -200,6 +200,23 @@ def test_spec_draft_prompt_lookup():
     assert R.spec_draft(hist, torch.tensor([5]), 2, 3).tolist() == [[11, 9, 10]]
 
 
+def test_spec_draft_latest_of_several_matches_wins():
+    """``engine/engine.py:973``: the latest match start (``max`` over candidates) is taken. The
+    suffix (1, 2) occurs at 0 and at 3 before the tail: the draft follows the one at 3 (7, 5), not
+    the one at 0 (9, 1)."""
+    hist = torch.tensor([[1, 2, 9, 1, 2, 7, 5, 1, 2, 0, 0]])
+    assert R.spec_draft(hist, torch.tensor([9]), 2, 2).tolist() == [[2, 7, 5]]
+    # a match that would overlap the suffix itself (start >= L - n) does not count: with the
+    # suffix (4, 4) at 4..5, the starts 0..3 qualify and the latest, 3, drafts hist[5:8] clamped
+    # to L - 1 = 5 -> (4, 4, 4); start 4 (the suffix itself) would draft past the history.
+    hist = torch.tensor([[4, 4, 4, 4, 4, 4, 0, 0]])
+    assert R.spec_draft(hist, torch.tensor([6]), 3, 2).tolist() == [[4, 4, 4, 4]]
+    # three occurrences, three rows with different valid lengths: each row's latest qualifying one
+    hist = torch.tensor([[5, 6, 1, 5, 6, 2, 5, 6, 3, 5, 6]] * 3)
+    L = torch.tensor([11, 8, 5])
+    assert R.spec_draft(hist, L, 1, 2).tolist() == [[6, 3], [6, 2], [6, 1]]
+
+
 def test_spec_accept():
     nxt = torch.tensor([[4, 5, 6, 9], [1, 2, 3, 4]])
     tok = torch.tensor([[0, 4, 5, 7], [0, 9, 9, 9]])
