@@ -88,12 +88,16 @@ def parse():
     p.add_argument("--profile-sample", action="store_true",
                    help="run only the dominant kernel of --config (c2: gate/up GEMV, c4: attention) and a plain "
                         "1 GiB device copy, for rocprofv3 --pmc traffic runs; prints one JSON line")
+    p.add_argument("--profile-kernel", default="dominant", choices=["dominant", "o"],
+                   help="with --profile-sample: the dominant kernel, or the O projection")
     return p.parse_args()
 
 
-def measured_traffic(config: str, kernel: str):
+def measured_traffic(config: str, kernel: str, nbytes: int | None = None):
     """HBM bytes per launch of ``kernel`` at ``config`` from the committed PMC summary
-    (``FETCH_SIZE`` + ``WRITE_SIZE`` scaled by a copy of known size), or None."""
+    (``FETCH_SIZE`` + ``WRITE_SIZE`` scaled by a copy of known size), or None. An entry measured at
+    another size (the attention's context grows during decoding) carries its algorithmic bytes, and
+    its traffic-to-algorithmic ratio is applied to ``nbytes``."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
@@ -102,6 +106,8 @@ def measured_traffic(config: str, kernel: str):
     entry = rec.get(config)
     if entry is None or entry.get("kernel") != kernel:
         return None
+    if nbytes is not None and entry.get("algorithmic_bytes"):
+        return int(round(entry["bytes_per_launch"] / entry["algorithmic_bytes"] * nbytes))
     return entry.get("bytes_per_launch")
 
 
@@ -143,6 +149,36 @@ def time_gate_up(eng, torch, reps=3, T=1):
     nbytes = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * (w0.N // 2) * 2
     name = ("gemv_kernel<%d, %d, true, 2>" % (M, b.gemv_cfg["gu"][1]) if b.gemv
             else ops.gemm_kernel_name(M, b.cfg["gu"], True, ops.EPI_SWIGLU))
+    return avg, nbytes, name
+
+
+def time_o_proj(eng, torch, reps=3):
+    """Average launch time of the O projection + residual (M = B rows, K = 4096), rotating over the 36
+    layers' weights. Returns (seconds, algorithmic bytes, kernel name)."""
+    from qwen_hip import ops
+    b = eng.bufs(eng.state.groups[0], 1)
+    a = b.a.view(b.M, -1)
+    h2 = b.h.clone()
+
+    def one(w):
+        if b.gemv:
+            ops.gemv(a, w.o_rows, residual=h2, out=h2, cfg=b.gemv_cfg["o"])
+        else:
+            ops.fused_linear(a, w.o, b.cfg["o"], residual=h2, out=h2, workspace=b.gemm_ws)
+
+    def sweep():
+        for w in eng.w.layers:
+            one(w)
+        return len(eng.w.layers)
+
+    sweep()
+    torch.cuda.synchronize()
+    avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
+    w0 = eng.w.layers[0].o
+    M = b.M
+    nbytes = w0.nbytes + M * w0.K * 2 + 2 * M * w0.N * 2
+    name = ("gemv_kernel<%d, %d, false, 1>" % (M, b.gemv_cfg["o"][1]) if b.gemv
+            else ops.gemm_kernel_name(M, b.cfg["o"], False, ops.EPI_RES))
     return avg, nbytes, name
 
 
@@ -254,7 +290,8 @@ def roofline(avg, nbytes, name, config, what):
     achieved = nbytes / avg
     return {"bound": "hbm", "kernel": f"{name}: {what}", "achieved": round(achieved / 1e9, 1),
             "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-            "traffic": measured_traffic(config, name), "avg_us": round(avg * 1e6, 2), "bytes_per_launch": int(nbytes)}
+            "traffic": measured_traffic(config, name, int(nbytes)), "avg_us": round(avg * 1e6, 2),
+            "bytes_per_launch": int(nbytes)}
 
 
 def bench_verify(eng, torch, cfg, B, S, K, W):
@@ -345,9 +382,12 @@ def cpu_baseline(eng, cfg, S, runs=3, target_s=6.0):
                        f"{runs} runs; host CPU {cpu}")}
 
 
-def profile_sample(eng, torch, config):
-    """Dominant-kernel launches plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
-    if config == "c4":
+def profile_sample(eng, torch, config, kernel="dominant"):
+    """Dominant-kernel (or ``kernel="o"``: O-projection) launches plus a copy of known size (the
+    FETCH_SIZE / WRITE_SIZE calibration)."""
+    if kernel == "o":
+        avg, nbytes, name = time_o_proj(eng, torch, reps=1)
+    elif config == "c4":
         avg, nbytes, name = time_attention(eng, torch, reps=1)
     else:
         avg, nbytes, name = time_gate_up(eng, torch, reps=1, T=SPEC_T if config == "c5" else 1)
@@ -388,7 +428,7 @@ def main():
         else:
             with torch.inference_mode():
                 eng.prepare(B, S, N + W + 1)
-        print(json.dumps(profile_sample(eng, torch, name)), flush=True)
+        print(json.dumps(profile_sample(eng, torch, name, args.profile_kernel)), flush=True)
         return
     if args.config == "c5":
         B, S, N = CONFIGS["c5"]

@@ -2,7 +2,7 @@
 
     python -m qwen_hip.rocprof_summary steps <run_kernel_trace.csv> [--last N] [--boundary NAME]
     python -m qwen_hip.rocprof_summary pmc <run_counter_collection.csv> --kernel SUBSTR
-                                           --copy-bytes B --copies C
+                                           --copy-bytes B --copies C [--last N]
 
 ``steps``: decode steps are the intervals between consecutive
 ``decode_finish_kernel`` dispatches (one per graph replay; ``spec_accept_kernel``
@@ -11,7 +11,8 @@ last N steps, each kernel's launches per step, average duration and share of
 the step, and the step-to-step time.
 
 ``pmc``: average of one counter (``FETCH_SIZE`` or ``WRITE_SIZE``, KiB per
-dispatch) over the dispatches whose name contains SUBSTR, next to the same
+dispatch) over the dispatches whose name contains SUBSTR (with ``--last N`` only the last N of
+them, in dispatch order: the profile sample's own launches), next to the same
 counter over the largest copy dispatches (``C`` copies of ``B`` bytes each way: the runtime's
 ``copyBuffer`` blits, else any copy-like kernel), and the scale factor ``B / (copy KiB * 1024)`` that turns the
 counter into bytes.
@@ -70,7 +71,7 @@ def steps(path: str, last: int, boundary: str = "decode_finish_kernel") -> str:
     return "\n".join(out)
 
 
-def pmc(path: str, kernel: str, copy_bytes: int, copies: int) -> str:
+def pmc(path: str, kernel: str, copy_bytes: int, copies: int, last: int = 0) -> str:
     rows = _rows(path)
     per = defaultdict(float)
     names = {}
@@ -80,7 +81,9 @@ def pmc(path: str, kernel: str, copy_bytes: int, copies: int) -> str:
         per[d] += float(r["Counter_Value"])
         names[d] = _short(r["Kernel_Name"])
         counter = r["Counter_Name"]
-    target = [per[d] for d in per if kernel in names[d]]
+    target = [per[d] for d in sorted(per) if kernel in names[d]]
+    if last > 0:   # only the last N dispatches (the profile sample), not engine set-up at other shapes
+        target = target[-last:]
     # the runtime's blit copy when present (other large elementwise kernels, such as a masked
     # fill of a KV-sized tensor, would otherwise pass for the calibration copy)
     copy_like = sorted(((per[d], d) for d in per if "copyBuffer" in names[d]), reverse=True) or \
@@ -112,8 +115,9 @@ def main():
     p.add_argument("--kernel", required=True)
     p.add_argument("--copy-bytes", type=int, required=True)
     p.add_argument("--copies", type=int, default=3)
+    p.add_argument("--last", type=int, default=0, help="average only the last N dispatches of the kernel")
     a = ap.parse_args()
-    print(steps(a.csv, a.last, a.boundary) if a.cmd == "steps" else pmc(a.csv, a.kernel, a.copy_bytes, a.copies))
+    print(steps(a.csv, a.last, a.boundary) if a.cmd == "steps" else pmc(a.csv, a.kernel, a.copy_bytes, a.copies, a.last))
 
 
 if __name__ == "__main__":
