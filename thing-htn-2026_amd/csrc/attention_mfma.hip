@@ -329,8 +329,9 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
 
   // One block: S = Q K^T, online softmax, O = O * alpha + P V. `vsrc` holds the block's V
   // rows in LDS (VROW stride); `visible(nt, row)` masks keys.
-  auto process = [&](const mu32x4 (&kf)[2][4], const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
-    f32x4_t s[MT][2];
+  // Split in two so that a block's registers can take the next block's loads as soon as its
+  // scores are computed: scores() reads K, finish() only the scores and the V rows in LDS.
+  auto scores = [&](const mu32x4 (&kf)[2][4], f32x4_t (&s)[MT][2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -340,6 +341,8 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
         for (int kt = 0; kt < 4; ++kt)
           s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[mt][kt], __builtin_bit_cast(bf16x8_t, kf[nt][kt]), s[mt][nt], 0, 0, 0);
       }
+  };
+  auto finish = [&](f32x4_t (&s)[MT][2], const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       float alpha[4];
@@ -393,6 +396,11 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
         o[mt][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[mt], as_bf16x8(vv), o[mt][nd], 0, 0, 0);
     }
   };
+  auto process = [&](const mu32x4 (&kf)[2][4], const bf16_t* vsrc, auto&& visible) __attribute__((always_inline)) {
+    f32x4_t s[MT][2];
+    scores(kf, s);
+    finish(s, vsrc, visible);
+  };
 
   // One cached block: its V rows to this wavefront's LDS tile, then S / softmax / PV.
   auto run_block = [&](const KVBlock& d, int blk) __attribute__((always_inline)) {
@@ -437,9 +445,18 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
     }
     if (blk < wb1) run_block(blkA, blk);
   } else {
+    // One block in flight: the next block's loads go out once this block's V rows are in LDS
+    // and its scores are computed (its registers are then free), ahead of the softmax and PV.
     for (int blk = wb0; blk < wb1; blk += BSTEP) {
-      run_block(blkA, blk);
+      const int kb = blk * MKB;
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the previous block's transpose reads come first
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *reinterpret_cast<mu32x4*>(vl + (4 * i + qq) * VROW + 8 * rr) = blkA.v[i];
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      f32x4_t s[MT][2];
+      scores(blkA.k, s);
       if (blk + BSTEP < wb1) load_block(blkA, (blk + BSTEP) * MKB);
+      finish(s, vl, [&](int nt, int row) { return kb + 16 * nt + rr < nold && row < R; });
     }
   }
   if constexpr (!NEW_FIRST) {
