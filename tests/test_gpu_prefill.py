@@ -93,7 +93,7 @@ def test_gemm_rejects_bad_shapes(qops):
 # ---------------------------------------------------------------- chunk attention
 
 @pytest.mark.parametrize("B,T,p0,Nkv", [(1, 1, 0, 8), (1, 5, 0, 8), (2, 16, 0, 2), (1, 100, 37, 8), (3, 64, 64, 2),
-                                        (2, 33, 500, 8), (1, 300, 1000, 1)])
+                                        (2, 33, 500, 8), (1, 300, 1000, 1), (2, 130, 0, 4), (1, 17, 3, 8)])
 def test_attn_prefill_matches_oracle(qops, B, T, p0, Nkv):
     g = torch.Generator().manual_seed(B * 1000 + T + p0)
     D, CAP = 128, p0 + T + 40
