@@ -401,29 +401,42 @@ __global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
 }
 
 
-// Second form of the prompt attention (used by qwen_attn_prefill): 8 wavefronts x 2 query tiles
-// per workgroup, i.e. 64 query tokens x the 4 heads of the GQA group = 256 query rows over the
-// same 64-key K / V block in LDS. Wavefront w owns tokens 8 w .. 8 w + 7 (tile mt: tokens
-// 8 w + 4 mt .. + 3). Every K fragment read from LDS feeds both tiles' QK^T MFMAs and every
-// transposed V fragment both tiles' PV MFMAs, which halves the LDS bytes per MFMA against one
-// tile per wavefront (the LDS port, not the matrix cores, bounded the one-tile form), and each
-// staged K / V byte serves four times as many query rows. Rounding points as pf_attn_kernel.
+// Wide form of the prompt attention (qwen_attn_prefill for chunks of more than 16 tokens):
+// 8 wavefronts x 2 query tiles per workgroup, i.e. 64 query tokens x the 4 heads of the GQA group
+// = 256 query rows over the same 64-key K / V block in LDS. Wavefront w owns tokens 8 w .. 8 w + 7
+// (tile mt: tokens 8 w + 4 mt .. + 3), so every K fragment read from LDS feeds both tiles' MFMAs
+// and each staged K / V byte serves four times as many query rows as in pf_attn_kernel.
 constexpr int AW2 = 8;               // wavefronts per workgroup
 constexpr int AQ2 = AW2 * 2 * 4;     // query tokens per workgroup (2 tiles of 4 tokens per wavefront)
 
-struct PfAttn2Smem {
-  union {
+// The score tiles are computed transposed, S^T = K Q^T (K as the MFMA's A operand, Q^T as B).
+// Lane (q, r) then holds query r's scores for keys 16 nt + 4 q + i, which is already the
+// B-operand layout of O^T += V^T P^T once the k-slots of the PV product are ordered (32 kk + 4 q + j, 32 kk + 16 + 4 q + j): P goes from the score
+// accumulators into the PV MFMA through packed bf16 conversions, with no LDS round trip, and the
+// V^T fragments are transposed LDS reads in that same key order. Softmax state is one (m, l)
+// per lane and tile; a query's 64 scores sit on 4 lanes (r, r + 16, r + 32, r + 48), so a block
+// maximum is 15 in-lane maxima and 2 cross-lane steps. The causal mask is applied only to blocks
+// that reach past the wavefront's first token. exp(x - m) is evaluated as exp2((x - m) log2 e)
+// with scale folded in; rounding points as pf_attn_kernel (P rounded to bf16 for PV, l from the
+// unrounded P, O normalised in fp32, then rounded). exp2 is the hardware v_exp_f32: a P below
+// 2^-126 of the block maximum flushes to 0, far under bf16's resolution of the row sum.
+__device__ __forceinline__ float xlane_max4(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float xlane_sum4(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+__global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams p) {
+  __shared__ union {
     struct {
       bf16_t k[2][AKB][AKROW];
       bf16_t v[2][AKB][AVROW];
     } kv;
     bf16_t ot[AW2][32][AKROW];       // output staging: 32 rows per wavefront
-  } u;
-  bf16_t pm[AW2][32][AKB];           // P of the wavefront's two tiles (rows 16 mt + ...)
-};
-
-__global__ void __launch_bounds__(AW2 * 64, 1) pf_attn2_kernel(PfAttnParams p) {
-  __shared__ PfAttn2Smem sm;
+  } sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qq = lane >> 4, rr = lane & 15;
@@ -440,21 +453,20 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn2_kernel(PfAttnParams p) {
   const bf16_t* kbase = p.kc + bh * (long long)p.CAP * AD;
   const bf16_t* vbase = p.vc + bh * (long long)p.CAP * AD;
 
-  // Q A-operand fragments: lane (q, r) of tile mt holds row r (token 8 wave + 4 mt + r / 4, head
-  // r % 4), dims 32 kt + 8 q .. +8. Tokens past T re-read token T - 1.
-  bf16x8_t qa[2][4];
+  // Q^T B-operand fragments: lane (q, r) of tile mt holds query r (token 8 wave + 4 mt + r / 4,
+  // head r % 4), dims 32 kt + 8 q .. +8. Tokens past T re-read token T - 1.
+  bf16x8_t qb8[2][4];
+  int my_last[2];                    // last key visible to this lane's query, per tile
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
-    const int t = min(t_lo + 8 * wave + 4 * mt + (rr >> 2), T - 1);
-    const bf16_t* qr = p.q + (((b * T + t) * Nq) + kvh * AG + (rr & 3)) * (long long)AD + 8 * qq;
+    const int tq = t_lo + 8 * wave + 4 * mt + (rr >> 2);
+    const bf16_t* qr = p.q + (((b * T + min(tq, T - 1)) * Nq) + kvh * AG + (rr & 3)) * (long long)AD + 8 * qq;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) qa[mt][kt] = as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * kt));
+    for (int kt = 0; kt < 4; ++kt) qb8[mt][kt] = as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * kt));
+    my_last[mt] = p.p0 + tq;
   }
-  // accumulator rows 4 qq + i of tile mt: token t_lo + 8 wave + 4 mt + qq, head i; its last
-  // visible key
-  int my_last[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) my_last[mt] = p.p0 + t_lo + 8 * wave + 4 * mt + qq;
+  const int wave_first = p.p0 + t_lo + 8 * wave;  // every query of the wavefront sees keys <= this
+  const float c = p.scale * 1.4426950408889634f;  // scale * log2(e)
 
   // K / V staging: thread -> 16-byte chunk c of keys (tid >> 4) + 32 i (keys past kmax are
   // read from slot 0 and their V rows zeroed, so a stale or non-finite slot never enters)
@@ -474,21 +486,17 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn2_kernel(PfAttnParams p) {
     for (int i = 0; i < 2; ++i) {
       const int kr = (tid >> 4) + 32 * i;
       const bool live = blk * AKB + kr < kmax;
-      *reinterpret_cast<pv4*>(&sm.u.kv.k[buf][kr][sc * 8]) = kst[i];
-      *reinterpret_cast<pv4*>(&sm.u.kv.v[buf][kr][sc * 8]) = live ? vst[i] : pv4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<pv4*>(&sm.kv.k[buf][kr][sc * 8]) = kst[i];
+      *reinterpret_cast<pv4*>(&sm.kv.v[buf][kr][sc * 8]) = live ? vst[i] : pv4{0u, 0u, 0u, 0u};
     }
   };
 
-  float m[2][4], l[2][4];
-  f32x4_t o[2][8];
+  float m[2] = {ANEG, ANEG}, l[2] = {0.f, 0.f};
+  f32x4_t o[2][8];                   // O^T: lane (q, r) holds dims 16 nd + 4 q + i of query r
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m[mt][i] = ANEG; l[mt][i] = 0.f; }
+  for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nd = 0; nd < 8; ++nd) o[mt][nd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  bf16_t* pl = &sm.pm[wave][0][0];
 
   load_kv(0);
   store_kv(0, 0);
@@ -498,74 +506,76 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn2_kernel(PfAttnParams p) {
     load_kv(nb);
     const int buf = blk & 1;
     const int kb0 = blk * AKB;
-    // S = Q K^T for 4 tiles of 16 keys: lane (q, r) takes key 16 nt + r, dims 32 kt + 8 q .. (one
-    // LDS read per (nt, kt), both query tiles)
-    f32x4_t s[2][4];
+    // S^T for 4 tiles of 16 keys: A = K rows 16 nt + r, dims 32 kt + 8 q (one LDS read per
+    // (nt, kt), both query tiles)
+    f32x4_t st[2][4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      s[0][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      s[1][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      st[0][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      st[1][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(&sm.u.kv.k[buf][16 * nt + rr][32 * kt + 8 * qq]);
-        s[0][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0][kt], as_bf16x8(kf), s[0][nt], 0, 0, 0);
-        s[1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1][kt], as_bf16x8(kf), s[1][nt], 0, 0, 0);
+        const uint4 kf = *reinterpret_cast<const uint4*>(&sm.kv.k[buf][16 * nt + rr][32 * kt + 8 * qq]);
+        st[0][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), qb8[0][kt], st[0][nt], 0, 0, 0);
+        st[1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), qb8[1][kt], st[1][nt], 0, 0, 0);
       }
     }
-    // online softmax per tile (rows 4 qq + i share the token, so one causal limit per lane)
+    if (kb0 + AKB - 1 > wave_first) {  // block reaches past some query's last key: mask
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kb0 + 16 * nt + 4 * qq + i > my_last[mt]) st[mt][nt][i] = ANEG;
+    }
+    // online softmax per tile (one query per lane); P^T as packed bf16 B fragments
+    uint4 pb[2][2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      float alpha[4];
+      float mx = st[mt][0][0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float sv[4];
-        float mx = ANEG;
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const bool vis = kb0 + 16 * nt + rr <= my_last[mt];
-          sv[nt] = vis ? s[mt][nt][i] * p.scale : ANEG;
-          mx = fmaxf(mx, sv[nt]);
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[mt][nt][i]);
+      mx = xlane_max4(mx);
+      const float mn = fmaxf(m[mt], mx);
+      const float mc = mn * c;
+      const float alpha = __builtin_amdgcn_exp2f(m[mt] * c - mc);
+      float pr[4][4];
+      float psum = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[nt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], c, -mc));  // masked: 0
+          psum += pr[nt][i];
         }
-        mx = prow16_max(mx);
-        const float mn = fmaxf(m[mt][i], mx);
-        alpha[i] = __expf(m[mt][i] - mn);
-        float psum = 0.f;
+      l[mt] = l[mt] * alpha + psum;
+      m[mt] = mn;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const float pr = sv[nt] > ANEG ? __expf(sv[nt] - mn) : 0.f;
-          psum += pr;
-          pl[(16 * mt + 4 * qq + i) * AKB + 16 * nt + rr] = f2bf(pr);  // P rounded to bf16 for PV
-        }
-        l[mt][i] = l[mt][i] * alpha[i] + psum;
-        m[mt][i] = mn;
-      }
+      for (int kk = 0; kk < 2; ++kk)
+        pb[mt][kk] = make_uint4(f2bf2(pr[2 * kk][0], pr[2 * kk][1]), f2bf2(pr[2 * kk][2], pr[2 * kk][3]),
+                                f2bf2(pr[2 * kk + 1][0], pr[2 * kk + 1][1]), f2bf2(pr[2 * kk + 1][2], pr[2 * kk + 1][3]));
 #pragma unroll
       for (int nd = 0; nd < 8; ++nd)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[mt][nd][i] *= alpha[i];
+        for (int i = 0; i < 4; ++i) o[mt][nd][i] *= alpha;
     }
-    // P in the A layout (lane (q, r): row r of tile mt, keys 32 kk + 8 q ..); the round trip
-    // stays inside the wavefront (LDS instructions complete in order)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    bf16x8_t pa[2][2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        pa[mt][kk] = as_bf16x8(*reinterpret_cast<const uint4*>(pl + (16 * mt + rr) * AKB + 32 * kk + 8 * qq));
-    // O += P V: V^T fragments by transpose reads (source lane s -> V[8 q + s / 4 (+4)][16 nd +
-    // 4 (s % 4)]), one read per (kk, nd) for both tiles
+    // O^T += V^T P^T: A = V^T rows (dims) 16 nd + r, k-slots j -> key 32 kk + 4 q + j (lo) and
+    // 32 kk + 16 + 4 q + j (hi), by transpose reads of 4 keys x 16 dims (source lane s ->
+    // V[32 kk + 4 q + s / 4 (+16)][16 nd + 4 (s % 4)]), one read pair per (kk, nd) for both tiles
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const bf16_t* vs = &sm.u.kv.v[buf][32 * kk + 8 * qq + (rr >> 2)][4 * (rr & 3)];
+      const bf16_t* vs = &sm.kv.v[buf][32 * kk + 4 * qq + (rr >> 2)][4 * (rr & 3)];
 #pragma unroll
       for (int nd = 0; nd < 8; ++nd) {
         const av4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 16 * nd));
-        const av4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 4 * AVROW + 16 * nd));
+        const av4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 16 * AVROW + 16 * nd));
         const uint4 vv = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                     __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
-        o[0][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0][kk], as_bf16x8(vv), o[0][nd], 0, 0, 0);
-        o[1][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1][kk], as_bf16x8(vv), o[1][nd], 0, 0, 0);
+        o[0][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), as_bf16x8(pb[0][kk]), o[0][nd], 0, 0, 0);
+        o[1][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), as_bf16x8(pb[1][kk]), o[1][nd], 0, 0, 0);
       }
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -573,24 +583,24 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn2_kernel(PfAttnParams p) {
     __syncthreads();
   }
 
-  // ---- normalise and write: the wavefront's 32 rows x 128 dims through LDS (bf16), 16-byte
-  // stores (the K / V buffers are free: every wavefront passed the loop's last barrier)
-  bf16_t* ot = &sm.u.ot[wave][0][0];
+  // ---- normalise and write: rows 16 mt + r (query r of tile mt) x 128 dims through LDS (bf16,
+  // 4 dims per 8-byte store), then 16-byte global stores (the K / V buffers are free: every
+  // wavefront passed the loop's last barrier)
+  bf16_t* ot = &sm.ot[wave][0][0];
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) l[mt][i] = prow16_sum(l[mt][i]);
+    const float inv = 1.f / xlane_sum4(l[mt]);
 #pragma unroll
     for (int nd = 0; nd < 8; ++nd)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ot[(16 * mt + 4 * qq + i) * AKROW + 16 * nd + rr] = f2bf(o[mt][nd][i] / l[mt][i]);
+      *reinterpret_cast<uint2*>(ot + (16 * mt + rr) * AKROW + 16 * nd + 4 * qq) =
+          make_uint2(f2bf2(o[mt][nd][0] * inv, o[mt][nd][1] * inv), f2bf2(o[mt][nd][2] * inv, o[mt][nd][3] * inv));
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
-    const int c = lane + 64 * it;        // 32 rows x 16 chunks
-    const int row = c >> 4, ch = c & 15;
+    const int cidx = lane + 64 * it;     // 32 rows x 16 chunks
+    const int row = cidx >> 4, ch = cidx & 15;
     const int t = t_lo + 8 * wave + (row >> 2);
     if (t < T) {
       const uint4 v = *reinterpret_cast<const uint4*>(ot + row * AKROW + ch * 8);
@@ -647,7 +657,7 @@ int qwen_attn_prefill(const void* q, const void* k_cache, const void* v_cache, v
   p.scale = scale;
   const long long blocks = p.bh_count * p.qblocks;
   if (blocks > 0x7fffffffLL) return QWEN_EARG;
-  if (wide) pf_attn2_kernel<<<dim3((unsigned)blocks), AW2 * 64, 0, stream>>>(p);
+  if (wide) pf_attn_wide_kernel<<<dim3((unsigned)blocks), AW2 * 64, 0, stream>>>(p);
   else pf_attn_kernel<<<dim3((unsigned)blocks), 256, 0, stream>>>(p);
   QWEN_RETURN_LAUNCH();
 }
