@@ -346,9 +346,9 @@ def tile_weight(w: torch.Tensor, pair: bool = False) -> TiledWeight:
 # MI355X (graph-replayed, 36 weight copies rotated), keyed by (N, K, SwiGLU
 # pair) and by M == 1, M <= 16 (one A fragment) or M <= 32 (two).
 _TUNED = {   # per M class: 1, <= 16, <= 24, <= 32 rows
-    (6144, 2560, False): {1: (2, 8, 1), 16: (2, 4, 1), 24: (2, 4, 1), 32: (4, 4, 2)},                  # QKV
-    (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 24: (1, 4, 1), 32: (2, 8, 3)},                  # O
-    (19456, 2560, True): {1: (2, 8, 1), 16: (8, 8, 1), 24: (2, 16, 256, 1), 32: (2, 16, 256, 1)},      # gate/up
+    (6144, 2560, False): {1: (2, 8, 1), 16: (2, 8, 1), 24: (2, 4, 1), 32: (4, 4, 2)},                  # QKV
+    (2560, 4096, False): {1: (1, 8, 1), 16: (1, 8, 1), 24: (2, 8, 3), 32: (2, 4, 3)},                  # O
+    (19456, 2560, True): {1: (2, 8, 1), 16: (2, 8, 1), 24: (2, 16, 256, 1), 32: (2, 16, 256, 1)},      # gate/up
     (2560, 9728, False): {1: (1, 16, 1), 16: (2, 4, 3), 24: (2, 4, 3), 32: (2, 4, 3)},                 # down
 }
 
