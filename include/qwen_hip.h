@@ -165,7 +165,8 @@ long long qwen_gemv_lds_bytes(int M, int N, int K, int grid, int waves, int epi)
  * computed in the kernel from x itself) and epilogue epi = 0 store, 1 residual add
  * (out = bf16(residual + bf16(acc)), residual may alias out), 2 SwiGLU (W = cat(gate, up)
  * rows [2N, K]; out = bf16(bf16(silu(bf16(g))) * bf16(u)), N columns), 3 argmax of the bf16
- * logits folded into amax[m] (same packed key as qwen_lm_head_argmax; out unused).
+ * logits folded into slot 0 of row m's key in amax (the key buffer of qwen_lm_head_argmax,
+ * QWEN_ARGMAX_KEYS(M) words; out unused).
  * Workgroup g of `grid` owns output rows [N*g/grid, N*(g+1)/grid), so every CU streams the
  * same bytes; K must be a multiple of 512; waves 8 or 16. Same operator contract as
  * qwen_linear / qwen_lm_head_argmax: replaces the projections of engine/engine.py:1108-1121
@@ -182,17 +183,26 @@ int qwen_gemv_rowmap(const void* x, const void* w, void* out, int M, int N, int 
                      float eps, const void* residual, int epi, unsigned long long* amax, const int32_t* row_map,
                      int grid, int waves, hipStream_t stream);
 
+/* Packed argmax keys of an M-row LM head: QWEN_ARGMAX_SLOTS slots per row, slot s of row m at
+ * amax[s * QWEN_ARGMAX_LD(M) + m] (uint64: monotone logit bits << 32 | ~index); the row's key
+ * is the maximum over its slots. A key buffer holds QWEN_ARGMAX_KEYS(M) words, zero before a
+ * producer runs; every consumer re-arms all slots of the rows it reads. */
+#define QWEN_ARGMAX_SLOTS 8
+#define QWEN_ARGMAX_LD(M) (((M) + 15) / 16 * 16)
+#define QWEN_ARGMAX_KEYS(M) (QWEN_ARGMAX_SLOTS * QWEN_ARGMAX_LD(M))
+
 /* Final RMSNorm + tied LM head + argmax over the bf16 logits (lowest index on ties):
  * token[m] = argmax_n bf16((rms_norm(x[m]) @ W^T)[n]); psq_in = x's qwen_sumsq16 partials.
- * The result is folded into amax[m] (uint64: monotone logit bits << 32 | ~index), which must
- * be zero before the call; with out_tok != NULL the tokens are extracted into out_tok [M]
- * int64 and amax re-armed, otherwise qwen_decode_finish / qwen_argmax_extract consume it.
+ * The result is folded into the key buffer amax (QWEN_ARGMAX_KEYS(M) words, workgroup g
+ * into slot g % QWEN_ARGMAX_SLOTS); with out_tok != NULL the tokens are extracted into out_tok
+ * [M] int64 and amax re-armed, otherwise qwen_decode_finish / qwen_argmax_extract consume it.
  * Replaces engine/engine.py:1119-1121 (final add_rms_norm, lm_head _mm, argmax). */
 int qwen_lm_head_argmax(const void* x, const void* norm_w, const float* psq_in, float eps, const void* w_tiled, int M,
                         int N, int K, unsigned long long* amax, int64_t* out_tok, int ntw, int waves,
                         hipStream_t stream);
 
-/* out[m] = token index held in amax[m] (from qwen_lm_head_argmax); re-arms amax to zero.
+/* out[m] = token index held in row m's key of amax (QWEN_ARGMAX_KEYS(M) words, from
+ * qwen_lm_head_argmax or qwen_gemv); re-arms the key buffer to zero.
  * Replaces the argmax(-1) read-out of engine/engine.py:1121. */
 int qwen_argmax_extract(unsigned long long* amax, int M, int64_t* out, hipStream_t stream);
 
@@ -203,7 +213,8 @@ int qwen_argmax_extract(unsigned long long* amax, int M, int64_t* out, hipStream
 int qwen_embed(const int64_t* tok, const int64_t* hist, const int32_t* pos, int cap, const void* w_tiled, void* out,
                float* psq_out, int M, long long V, int K, hipStream_t stream);
 
-/* Step tail after the LM head: token[b] = index held in amax[b] (re-armed to zero) -> next[b];
+/* Step tail after the LM head: token[b] = index held in row b's key of amax (QWEN_ARGMAX_KEYS(B)
+ * words, re-armed to zero) -> next[b];
  * hist[b, pos[b]+1] = token[b], pos[b] += 1, frozen rows ((pos+1 - s_buf) >= ntarget) write slot
  * cap-1 and keep pos; then h[b] = W[hist[b, pos[b]]] from the tiled table and psq its
  * qwen_sumsq16 partials (the next step's input). Replaces the tail of engine/engine.py:941-953

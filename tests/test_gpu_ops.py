@@ -448,8 +448,16 @@ def test_decode_finish_updates_history_and_embeds(qops):
     table = _bf16(V, K, gen=g)
     t = qops.tile_weight(table.to(DEV))
     toks = [17, 95, 0]
-    keys = torch.tensor([_argmax_key(1.5, toks[0]), _argmax_key(-0.25, toks[1]), _argmax_key(0.0, toks[2])],
-                        dtype=torch.int64, device=DEV)
+    # Row b's winning key sits in slot 3 b % 8 (slot s of row m at s * ld + m) and a smaller key
+    # (a lower logit, or the same logit at a higher index) in another slot: the consumer takes
+    # the maximum over the slots and re-arms every slot.
+    ld = (B + 15) // 16 * 16
+    kcpu = torch.zeros(qops.argmax_keys_count(B), dtype=torch.int64)
+    for b, (logit, lose) in enumerate([(1.5, _argmax_key(1.25, 3)), (-0.25, _argmax_key(-0.25, 96)),
+                                       (0.0, _argmax_key(-7.0, 1))]):
+        kcpu[(3 * b % 8) * ld + b] = _argmax_key(logit, toks[b])
+        kcpu[((3 * b + 5) % 8) * ld + b] = lose
+    keys = kcpu.to(DEV)
     hist = torch.randint(0, V, (B, cap), generator=g)
     pos = torch.tensor([3, 9, 12], dtype=torch.int32)
     s_buf = torch.tensor([3], dtype=torch.int64)

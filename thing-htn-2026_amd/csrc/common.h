@@ -39,6 +39,28 @@ __device__ __forceinline__ uint32_t f2bf2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
+// Packed argmax keys (monotone logit bits << 32 | ~index) of an M-row LM head are spread over
+// ARGMAX_SLOTS slots per row: slot s of row m at s * argmax_ld(M) + m, so two slots are at least
+// a 128-byte line apart. Workgroup g folds its rows' keys into slot g % ARGMAX_SLOTS, which
+// spreads the launch's 64-bit atomicMax operations over ARGMAX_SLOTS addresses per row instead
+// of one (same-address atomics serialise: ~25 us of a 194 us LM head at M = 32, measured); the
+// consumers take the maximum over the slots and re-arm all of them to zero.
+constexpr int ARGMAX_SLOTS = 8;
+__host__ __device__ __forceinline__ int argmax_ld(int M) { return (M + 15) / 16 * 16; }
+__device__ __forceinline__ unsigned long long argmax_key(const unsigned long long* amax, int M, int m) {
+  unsigned long long k = 0;
+#pragma unroll
+  for (int s = 0; s < ARGMAX_SLOTS; ++s) {
+    const unsigned long long v = amax[(long long)s * argmax_ld(M) + m];
+    k = v > k ? v : k;
+  }
+  return k;
+}
+__device__ __forceinline__ void argmax_rearm(unsigned long long* amax, int M, int m) {
+#pragma unroll
+  for (int s = 0; s < ARGMAX_SLOTS; ++s) amax[(long long)s * argmax_ld(M) + m] = 0ull;
+}
+
 // Round an fp32 value to the nearest bf16 and return it widened again.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 

@@ -309,7 +309,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
         if (r == 0 && mok) {
           const unsigned long long key =
               ((unsigned long long)ordered_bits(best) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)bidx);
-          __hip_atomic_fetch_max(p.amax + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_max(p.amax + (long long)(blockIdx.x % ARGMAX_SLOTS) * argmax_ld(p.M) + m, key,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       } else {
         bf16_t* orow = p.out + (size_t)(mok ? m : 0) * p.ld_out;
@@ -820,14 +821,15 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
   }
 }
 
-// token[m] = index held in a packed argmax key; the key is re-armed to zero.
+// token[m] = index held in row m's packed argmax key (the maximum over its slots); the slots
+// are re-armed to zero.
 __global__ void __launch_bounds__(64) argmax_extract_kernel(unsigned long long* __restrict__ amax, int M,
                                                             int64_t* __restrict__ out) {
   const int m = blockIdx.x * 64 + threadIdx.x;
   if (m >= M) return;
-  const unsigned long long key = amax[m];
+  const unsigned long long key = argmax_key(amax, M, m);
   out[m] = (int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
-  amax[m] = 0ull;
+  argmax_rearm(amax, M, m);
 }
 
 template <int MT, int NTW, int WPG, bool NORM, int EPI>

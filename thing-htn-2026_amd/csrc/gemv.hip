@@ -40,7 +40,7 @@ struct GemvParams {
   const bf16_t* nw;     // [K] RMSNorm gain (NORM)
   const bf16_t* res;    // [M, ld_out] residual (GEPI_RES; may alias out)
   bf16_t* out;          // [M, ld_out]
-  unsigned long long* amax;  // [M] packed argmax keys (GEPI_ARGMAX), zero before the launch
+  unsigned long long* amax;  // packed argmax keys (GEPI_ARGMAX, slot 0 of each row), zero before the launch
   const int32_t* rowmap;     // [N] output column of weight row i (GEPI_STORE; nullptr: column i)
   int N, K, ld_out;     // N = output columns (SwiGLU: gate/up row pairs)
   float eps;

@@ -3,7 +3,7 @@
 // Restates the tail of engine/engine.py:941-953 (_plain_step after the model
 // step) and the head of the next step (engine/engine.py:1101, the embedding of
 // hist[pos]), fused into one launch that follows the LM head:
-//   token[b]   = index held in the packed argmax key amax[b] (re-armed to zero)
+//   token[b]   = index held in row b's packed argmax key (its slots re-armed to zero)
 //   hist[b, pos[b] + 1] = token[b] and pos[b] += 1, unless the sequence already
 //   produced its max_new_tokens (frozen rows write to the dump slot cap-1 and
 //   keep their position)
@@ -21,7 +21,7 @@ __global__ void __launch_bounds__(FIN_THREADS) decode_finish_kernel(
     const bf16_t* __restrict__ w, bf16_t* __restrict__ h, float* __restrict__ psq, int cap, long long V, int K) {
   const int b = blockIdx.x;
   // Every thread reads the state before thread 0 updates it.
-  const unsigned long long key = amax[b];
+  const unsigned long long key = argmax_key(amax, gridDim.x, b);
   const int64_t tok = (int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   const long long p0 = pos[b];
   const long long L = p0 + 1;
@@ -35,7 +35,7 @@ __global__ void __launch_bounds__(FIN_THREADS) decode_finish_kernel(
     hist[(long long)b * cap + idx] = tok;
     if (!done) pos[b] = (int32_t)L;
     next[b] = tok;
-    amax[b] = 0ull;
+    argmax_rearm(amax, gridDim.x, b);
   }
   // Embedding gather from the tiled table (ids clamped into [0, V)).
   embed_row_tiled(w, id, V, K, h + (long long)b * K, psq + (long long)b * (K / 16), threadIdx.x, FIN_THREADS);

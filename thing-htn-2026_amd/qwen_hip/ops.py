@@ -603,7 +603,7 @@ def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, res
     if amax is not None:
         epi = GEPI_ARGMAX
         assert norm_w is not None and residual is None and not silu_pair
-        assert amax.dtype == torch.int64 and amax.numel() >= M and amax.is_contiguous()
+        assert amax.dtype == torch.int64 and amax.numel() >= argmax_keys_count(M) and amax.is_contiguous()
     elif silu_pair:
         epi = GEPI_SWIGLU
         assert norm_w is not None and residual is None and w.shape[0] % 2 == 0
@@ -647,9 +647,17 @@ def lm_head_config(M: int, N: int, K: int) -> tuple[int, int]:
     return (1, 8)
 
 
+ARGMAX_SLOTS = 8   # QWEN_ARGMAX_SLOTS: key slots per row (atomics of the LM head spread over them)
+
+
+def argmax_keys_count(M: int) -> int:
+    """Words of an M-row key buffer (``QWEN_ARGMAX_KEYS``): slot s of row m at s * ld + m."""
+    return ARGMAX_SLOTS * ((M + 15) // 16 * 16)
+
+
 def argmax_keys(M: int, device) -> torch.Tensor:
-    """Packed (logit, index) argmax keys, zeroed; every consumer re-arms them to zero."""
-    return torch.zeros((M,), dtype=torch.int64, device=device)
+    """Packed (logit, index) argmax keys of M rows, zeroed; every consumer re-arms them."""
+    return torch.zeros((argmax_keys_count(M),), dtype=torch.int64, device=device)
 
 
 def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWeight, *, cfg=None,
@@ -669,7 +677,7 @@ def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWe
     ntw, waves = cfg if cfg is not None else lm_head_config(M, w.N, K)
     if keys is None:
         keys = argmax_keys(M, x.device)
-    assert keys.dtype == torch.int64 and keys.numel() >= M and keys.is_contiguous()
+    assert keys.dtype == torch.int64 and keys.numel() >= argmax_keys_count(M) and keys.is_contiguous()
     if extract and out is None:
         out = torch.empty((M,), dtype=torch.int64, device=x.device)
     _lib.call("qwen_lm_head_argmax", x.data_ptr(), norm_w.data_ptr(), psq_in.data_ptr(), float(eps),
@@ -680,6 +688,7 @@ def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: TiledWe
 
 def argmax_extract(keys: torch.Tensor, M: int, out: torch.Tensor) -> torch.Tensor:
     """Tokens of packed argmax keys (re-arms the keys to zero)."""
+    assert keys.dtype == torch.int64 and keys.numel() >= argmax_keys_count(M) and keys.is_contiguous()
     _lib.call("qwen_argmax_extract", keys.data_ptr(), int(M), out.data_ptr(), _stream())
     return out
 
@@ -688,6 +697,7 @@ def decode_finish(keys, nxt, hist, pos, s_buf, ntarget, w: TiledWeight, h, psq) 
     """Step tail (``engine/engine.py:941-953``) + next step's embedding: token from the
     argmax keys, history / position update, ``h = W[hist[pos]]`` and its statistics."""
     B, cap = hist.shape
+    assert keys.dtype == torch.int64 and keys.numel() >= argmax_keys_count(B) and keys.is_contiguous()
     _lib.call("qwen_decode_finish", keys.data_ptr(), nxt.data_ptr(), hist.data_ptr(), pos.data_ptr(),
               s_buf.data_ptr(), ntarget.data_ptr(), w.data.data_ptr(), h.data_ptr(), psq.data_ptr(), B, cap, w.N,
               w.K, _stream())
