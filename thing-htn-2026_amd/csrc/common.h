@@ -163,5 +163,18 @@ __device__ __forceinline__ void store16_dev(__amdgpu_buffer_rsrc_t r, int off, f
 
 static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
 
+// Compute units of the current device (cached per device and translation unit; 0 on error).
+static inline int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Launch-status check used by every entry point: returns the launch error.
 #define QWEN_RETURN_LAUNCH() return qwen_status(hipGetLastError())

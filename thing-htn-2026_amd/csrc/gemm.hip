@@ -855,18 +855,7 @@ int dispatch_sk(const GemmParams& p, int grid, int mt, int ntw, hipStream_t stre
   return QWEN_EARG;
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
+int cu_count() { return device_cu_count(); }
 
 // Stream-K applies when every CU gets at least one tile, a unit spans at most
 // SK_PIECES CUs and a wavefront's share touches at most two units.

@@ -196,6 +196,215 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(PfGemmParams p) {
   }
 }
 
+
+// Wide form of the prompt GEMM (qwen_gemm for N a multiple of 256): a workgroup of 4
+// wavefronts computes a 256-row x 256-column tile, wavefront (wm, wn) a 128 x 128 quadrant
+// (8 x 8 accumulator tiles, 256 registers: they live in the AGPRs, one wavefront per SIMD).
+// Both operands are staged in LDS per k-step of 64 (double buffered, 2 x 64 KB): A rows as in
+// pf_gemm_kernel (16-byte chunk c of row r at slot c ^ (r % 8)), W as its 1 KB MFMA tiles in
+// their global order. Per k-step and CU that is 64 KB from L2 for 8.4 MFLOP, half of
+// pf_gemm_kernel's traffic per flop, and 128 KB of LDS fragment reads against 2048 MFMA cycles
+// per SIMD. The product is computed transposed, D^T = W X^T: a weight tile is the MFMA's A
+// operand as it stands (lane (q, r): row r, k 8 q ..) and an A-row fragment its B operand, so
+// lane (q, r) of accumulator tile (mb, nb) holds D[16 mb + r][16 nb + 4 q + i], four adjacent
+// output columns of one row: the epilogue writes them as one 8-byte store (SwiGLU pairs the
+// gate and up tiles 2 p, 2 p + 1 of the pair-interleaved weight element by element).
+// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at LDS byte address
+// `lds_addr` + 16 l (lds_addr wavefront-uniform, held in M0). Written as inline assembly so that
+// the compiler does not treat it as an LDS store: it would otherwise make every later LDS read
+// wait for all such loads. The caller therefore waits for them itself (lds_dma_wait) before
+// the barrier after which they are read; waits the compiler places for its own loads stay
+// correct, only more conservative (loads complete in issue order). s_nop covers the M0 write ->
+// LDS-DMA hazard.
+__device__ __forceinline__ void lds_dma16(const void* gptr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gptr), "s"(lds_addr)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+constexpr int PWM = 256;   // rows per workgroup
+constexpr int PWN = 256;   // weight rows (output columns before SwiGLU) per workgroup
+constexpr int PWG = 4;     // row tiles per group of the wide kernel's tile walk
+
+template <int EPI>
+__global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
+  __shared__ pv4 lds[2 * (PWM + PWN) * (PBK / 8)];  // [stage][A: 256 rows x 8 chunks | W: 32 tiles x 64 lanes]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int qq = lane >> 4, rr = lane & 15;
+
+  // Persistent tile walk: gridDim.x = 8 s workgroups, workgroup g on XCD g % 8 (one per CU).
+  // XCD x owns the contiguous run of logical tiles [x * ceil(T / 8), ...); its s workgroups take
+  // them s at a time (workgroup g: run positions g / 8, g / 8 + s, ...). Logical tiles go in
+  // groups of PWG row tiles, the row tile fastest, so the tiles an XCD works on at one time
+  // form a block of PWG row tiles x s / PWG column tiles and share A and W k-slabs in its L2.
+  // A workgroup keeps its CU from tile to tile: the next tile's first k-step is loaded while the
+  // current tile's last one computes, and the current tile's output stores drain while the next
+  // tile's MFMAs run (no workgroup turnover, no chip-wide burst of epilogue stores).
+  const int tiles = p.mtiles * p.ntiles;
+  const int per_xcd = (tiles + 7) / 8;
+  const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3), nslots = (int)(gridDim.x >> 3);
+  const int KT = p.K / 32, KB = p.K / PBK;
+  auto tile_at = [&](int step, long long& m0, int& nt0) -> bool {
+    const int j = slot + step * nslots;
+    const int lt = xcd * per_xcd + j;
+    if (j >= per_xcd || lt >= tiles) return false;
+    const int gsize = PWG * p.ntiles;
+    const int grp = lt / gsize;
+    const int rem = lt - grp * gsize;
+    const int gsz = min(PWG, p.mtiles - grp * PWG);
+    m0 = (long long)(grp * PWG + rem % gsz) * PWM;
+    nt0 = (rem / gsz) * (PWN / 16);  // the tile's first weight n-tile
+    return true;
+  };
+
+  // Staging by direct global -> LDS loads (16 bytes per lane; one instruction fills 1 KB of LDS,
+  // lane l at byte 16 l): wavefront w fills A blocks 8 w .. 8 w + 7 (block b = rows 8 b .. 8 b + 7;
+  // lane l loads chunk (l % 8) ^ (l / 8) of row 8 b + l / 8, which lands in the swizzled slot
+  // l % 8 of that row) and W tiles 8 w .. 8 w + 7 of the k-step (tile t = 2 j + kt, stored as
+  // in memory). Rows past M re-read row M - 1 and are never stored. No staging registers.
+  // (M * K < 2^31 is checked by the host.)
+  // Addresses are formed per load from the tile's origin (m0, nt0), both wavefront-uniform:
+  // arrays of per-tile offsets kept across the tile loop would live in scratch memory.
+  const int achunk = ((lane & 7) ^ (lane >> 3)) * 8;
+  const int arow = wave * 64 + (lane >> 3);  // + 8 i: this lane's row of A block 8 wave + i
+  const pv4* wlane = reinterpret_cast<const pv4*>(p.w) + lane;
+  // LDS byte address of stage 0 (stage 1 follows it)
+  const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)lds;
+  auto issue = [&](long long m0, int nt0, int kb, int buf) __attribute__((always_inline)) {
+    const unsigned sb = lds0 + buf * ((PWM + PWN) * 8 * 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const long long row = min(m0 + arow + 8 * i, (long long)p.M - 1);
+      lds_dma16(p.a + (int)row * p.K + achunk + kb * PBK, sb + (wave * 8 + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = wave * 8 + i;
+      lds_dma16(wlane + ((long long)(nt0 + (t >> 1)) * KT + kb * 2 + (t & 1)) * 64, sb + (PWM * 8 + t * 64) * 16);
+    }
+  };
+
+  f32x4_t acc[8][8];
+
+  // One k-step on stage `buf`: the first half k-step's 16 fragments (8 W, 8 A-row) are read,
+  // the following stage's loads go out (behind those reads: ahead of them they would hold the
+  // reads up in the LDS queue; that stage was last read one k-step ago), then the half's MFMAs
+  // run in groups of 8 (one A-row fragment each) with two of the second half's fragments
+  // requested after each group, so the LDS reads overlap the matrix cores and no wait needs more
+  // than 15 LDS requests outstanding (the counter's limit). The scheduling barriers pin that
+  // order.
+  auto kstep = [&](int buf, bool nload, long long nm0, int nnt0, int nkb) __attribute__((always_inline)) {
+    const pv4* cur = lds + buf * ((PWM + PWN) * 8);
+    auto wfrag = [&](int kt, int nb) { return __builtin_bit_cast(bf16x8_t, cur[PWM * 8 + ((wn * 8 + nb) * 2 + kt) * 64 + lane]); };
+    auto xfrag = [&](int kt, int mb) {
+      const int row = wm * 128 + mb * 16 + rr;
+      return __builtin_bit_cast(bf16x8_t, cur[row * 8 + ((kt * 4 + qq) ^ (row & 7))]);
+    };
+    bf16x8_t w0[8], x0[8], w1[8], x1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w0[j] = wfrag(0, j);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x0[j] = xfrag(0, j);
+    if (nload) issue(nm0, nnt0, nkb, buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[nb], x0[mb], acc[mb][nb], 0, 0, 0);
+      w1[mb] = wfrag(1, mb);
+      x1[mb] = xfrag(1, mb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[nb], x1[mb], acc[mb][nb], 0, 0, 0);
+    }
+    // The MFMAs only touch registers, so the scheduler may sink them below the barrier and the
+    // wait for the loads issued above; this keeps them ahead (they run while the loads fly).
+    __builtin_amdgcn_sched_barrier(0);
+    lds_dma_wait();  // this wavefront's loads have landed in LDS ...
+    __syncthreads();  // ... and, past the barrier, every wavefront's
+  };
+
+  // Epilogue of the tile at (m0, nt0): lane (q, r) of accumulator tile (mb, nb) holds
+  // D[16 mb + r][16 nb + 4 q + i] of the wavefront's quadrant; four adjacent columns -> one
+  // 8-byte store.
+  auto epilogue = [&](long long m0, int nt0) __attribute__((always_inline)) {
+  #pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const long long grow = m0 + wm * 128 + mb * 16 + rr;
+      if (grow >= p.M) continue;
+      if constexpr (EPI == PEPI_SWIGLU) {
+  #pragma unroll
+        for (int pj = 0; pj < 4; ++pj) {
+          float o[4];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = rbf(acc[mb][2 * pj][i]);
+            const float u = rbf(acc[mb][2 * pj + 1][i]);
+            const float sg = rbf(g / (1.0f + expf(-g)));
+            o[i] = mul_rn(sg, u);
+          }
+          const long long col = (long long)(nt0 / 2 + wn * 4 + pj) * 16 + 4 * qq;
+          *reinterpret_cast<uint2*>(p.out + grow * p.ldo + col) = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
+        }
+      } else {
+  #pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const long long col = (long long)(nt0 + wn * 8 + nb) * 16 + 4 * qq;
+          float o[4];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = acc[mb][nb][i];
+          if constexpr (EPI == PEPI_RES) {
+            const uint2 rv = *reinterpret_cast<const uint2*>(p.res + grow * p.ldo + col);
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t w2 = i < 2 ? rv.x : rv.y;
+              const float r = __uint_as_float((i & 1) ? (w2 & 0xffff0000u) : (w2 << 16));
+              o[i] = add_rn(r, rbf(o[i]));
+            }
+          }
+          *reinterpret_cast<uint2*>(p.out + grow * p.ldo + col) = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
+        }
+      }
+    }
+  };
+
+  long long m0;
+  int nt0;
+  if (!tile_at(0, m0, nt0)) return;
+  issue(m0, nt0, 0, 0);
+  lds_dma_wait();
+  __syncthreads();
+  int buf = 0;
+  for (int step = 0;; ++step) {
+    long long m1 = 0;
+    int nt1 = 0;
+    const bool more = tile_at(step + 1, m1, nt1);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb + 1 < KB; ++kb) {  // the next stage is this tile's k-step kb + 1
+      kstep(buf, true, m0, nt0, kb + 1);
+      buf ^= 1;
+    }
+    kstep(buf, more, m1, nt1, 0);  // last k-step: the next stage is the next tile's first
+    buf ^= 1;
+    epilogue(m0, nt0);
+    if (!more) break;
+    m0 = m1;
+    nt0 = nt1;
+  }
+}
+
 // ------------------------------------------------------------------ causal flash attention
 constexpr int AD = 128;      // head dim
 constexpr int AG = 4;        // query heads per KV head
@@ -628,11 +837,22 @@ int qwen_gemm(const void* a, const void* w_tiled, void* out, int M, int N, int K
   p.res = (const bf16_t*)residual;
   p.out = (bf16_t*)out;
   p.M = M; p.N = N; p.K = K; p.ldo = ld_out;
-  p.mtiles = (M + PBM - 1) / PBM;
-  p.ntiles = N / PBN;
-  const long long blocks = (long long)p.mtiles * p.ntiles;
+  const bool wide = N % PWN == 0;
+  p.mtiles = (M + (wide ? PWM : PBM) - 1) / (wide ? PWM : PBM);
+  p.ntiles = N / (wide ? PWN : PBN);
+  long long blocks = (long long)p.mtiles * p.ntiles;
   if (blocks > 0x7fffffffLL) return QWEN_EARG;
+  if (wide) {  // persistent: one workgroup per CU (8 per XCD round), at most one per tile of an XCD's run
+    const long long per_xcd = (blocks + 7) / 8;
+    blocks = 8 * std::min<long long>(per_xcd, std::max(1, device_cu_count() / 8));
+  }
   const dim3 grid((unsigned)blocks);
+  if (wide) {
+    if (epi == PEPI_STORE) pf_gemm_wide_kernel<PEPI_STORE><<<grid, 256, 0, stream>>>(p);
+    else if (epi == PEPI_RES) pf_gemm_wide_kernel<PEPI_RES><<<grid, 256, 0, stream>>>(p);
+    else pf_gemm_wide_kernel<PEPI_SWIGLU><<<grid, 256, 0, stream>>>(p);
+    QWEN_RETURN_LAUNCH();
+  }
   if (epi == PEPI_STORE) pf_gemm_kernel<PEPI_STORE><<<grid, 256, 0, stream>>>(p);
   else if (epi == PEPI_RES) pf_gemm_kernel<PEPI_RES><<<grid, 256, 0, stream>>>(p);
   else pf_gemm_kernel<PEPI_SWIGLU><<<grid, 256, 0, stream>>>(p);
