@@ -274,29 +274,29 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
   const pv4* wlane = reinterpret_cast<const pv4*>(p.w) + lane;
   // LDS byte address of stage 0 (stage 1 follows it)
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)lds;
-  auto issue = [&](long long m0, int nt0, int kb, int buf) __attribute__((always_inline)) {
+  // Loads i of a stage (i = 0 .. 7): the wavefront's A block 8 wave + i and W tile 8 wave + i.
+  auto issue_pair = [&](long long m0, int nt0, int kb, int buf, int i) __attribute__((always_inline)) {
     const unsigned sb = lds0 + buf * ((PWM + PWN) * 8 * 16);
+    const long long row = min(m0 + arow + 8 * i, (long long)p.M - 1);
+    lds_dma16(p.a + (int)row * p.K + achunk + kb * PBK, sb + (wave * 8 + i) * 1024);
+    const int t = wave * 8 + i;
+    lds_dma16(wlane + ((long long)(nt0 + (t >> 1)) * KT + kb * 2 + (t & 1)) * 64, sb + (PWM * 8 + t * 64) * 16);
+  };
+  auto issue = [&](long long m0, int nt0, int kb, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const long long row = min(m0 + arow + 8 * i, (long long)p.M - 1);
-      lds_dma16(p.a + (int)row * p.K + achunk + kb * PBK, sb + (wave * 8 + i) * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = wave * 8 + i;
-      lds_dma16(wlane + ((long long)(nt0 + (t >> 1)) * KT + kb * 2 + (t & 1)) * 64, sb + (PWM * 8 + t * 64) * 16);
-    }
+    for (int i = 0; i < 8; ++i) issue_pair(m0, nt0, kb, buf, i);
   };
 
   f32x4_t acc[8][8];
 
   // One k-step on stage `buf`: the first half k-step's 16 fragments (8 W, 8 A-row) are read,
-  // the following stage's loads go out (behind those reads: ahead of them they would hold the
-  // reads up in the LDS queue; that stage was last read one k-step ago), then the half's MFMAs
-  // run in groups of 8 (one A-row fragment each) with two of the second half's fragments
-  // requested after each group, so the LDS reads overlap the matrix cores and no wait needs more
-  // than 15 LDS requests outstanding (the counter's limit). The scheduling barriers pin that
-  // order.
+  // then the half's MFMAs run in groups of 8 (one A-row fragment each). After each group two of
+  // the second half's fragments are requested, so the LDS reads overlap the matrix cores and no
+  // wait needs more than 15 LDS requests outstanding (the counter's limit), and two of the
+  // following stage's 16 direct loads go out (that stage was last read one k-step ago): issued
+  // back to back, 64 loads of 1 KB per CU hold each wavefront at issue while the address unit
+  // works through them (measured: the k-step then takes 1.6x its MFMA time), spread out they run
+  // under the MFMAs. The scheduling barriers pin that order.
   auto kstep = [&](int buf, bool nload, long long nm0, int nnt0, int nkb) __attribute__((always_inline)) {
     const pv4* cur = lds + buf * ((PWM + PWN) * 8);
     auto wfrag = [&](int kt, int nb) { return __builtin_bit_cast(bf16x8_t, cur[PWM * 8 + ((wn * 8 + nb) * 2 + kt) * 64 + lane]); };
@@ -309,7 +309,6 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
     for (int j = 0; j < 8; ++j) w0[j] = wfrag(0, j);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x0[j] = xfrag(0, j);
-    if (nload) issue(nm0, nnt0, nkb, buf ^ 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
@@ -318,6 +317,7 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[nb], x0[mb], acc[mb][nb], 0, 0, 0);
       w1[mb] = wfrag(1, mb);
       x1[mb] = xfrag(1, mb);
+      if (nload) issue_pair(nm0, nnt0, nkb, buf ^ 1, mb);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
