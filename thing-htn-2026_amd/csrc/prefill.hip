@@ -639,20 +639,33 @@ __device__ __forceinline__ float xlane_sum4(float v) {
 }
 
 __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams p) {
+  // K / V blocks in 256-byte rows with no padding (direct-to-LDS loads fill 1 KB runs), swizzled
+  // so that the fragment reads stay conflict-free: K's 16-byte chunk c of key row r at c ^ (r % 16)
+  // (the S^T operand reads 16 rows of one chunk), V's 32-byte block j of row r at j ^ (r % 8) (a
+  // transposed read takes 8 bytes from 4 consecutive rows of one block, two groups of lanes at
+  // once take rows 4 apart).
   __shared__ union {
     struct {
-      bf16_t k[2][AKB][AKROW];
-      bf16_t v[2][AKB][AVROW];
+      pv4 k[2][AKB][16];
+      pv4 v[2][AKB][16];
     } kv;
     bf16_t ot[AW2][32][AKROW];       // output staging: 32 rows per wavefront
   } sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qq = lane >> 4, rr = lane & 15;
-  // heaviest query blocks first
-  const long long id = blockIdx.x;
-  const int qb = p.qblocks - 1 - (int)(id / p.bh_count);
-  const long long bh = id % p.bh_count;
+  // Launch order: workgroup g runs on XCD g % 8 and takes logical item (g % 8) * ceil(G / 8) +
+  // g / 8, so each XCD walks a contiguous run of items; an item is (head group bh, query block),
+  // all query blocks of a head group consecutive, heaviest first. The workgroups that read the
+  // same K / V (every query block of one head group) then run at the same time on one XCD and
+  // stream its blocks in step, through that XCD's L2, instead of each reading them from HBM in
+  // a different round.
+  const long long G = p.bh_count * p.qblocks;
+  const long long per_xcd = (G + 7) / 8;
+  const long long item = (long long)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (item >= G) return;
+  const long long bh = item / p.qblocks;
+  const int qb = p.qblocks - 1 - (int)(item - bh * p.qblocks);
   const long long b = bh / p.Nkv;
   const int kvh = (int)(bh - b * p.Nkv);
   const int T = p.T, Nq = p.Nkv * AG;
@@ -677,26 +690,25 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
   const int wave_first = p.p0 + t_lo + 8 * wave;  // every query of the wavefront sees keys <= this
   const float c = p.scale * 1.4426950408889634f;  // scale * log2(e)
 
-  // K / V staging: thread -> 16-byte chunk c of keys (tid >> 4) + 32 i (keys past kmax are
-  // read from slot 0 and their V rows zeroed, so a stale or non-finite slot never enters)
-  const int sc = tid & 15;
-  pv4 kst[2], vst[2];
-  auto load_kv = [&](int blk) __attribute__((always_inline)) {
+  // K / V staging by direct global -> LDS loads: wavefront w fills key rows 8 w .. 8 w + 7 of a
+  // block (two 1 KB runs of 4 rows each for K and for V); lane l lands at row 4 (2 w + i) + l / 16,
+  // physical chunk l % 16, so it loads the logical chunk the swizzle puts there. Keys past kmax
+  // read slot 0, a finite row every query's P weighs with exactly 0, so a stale or non-finite
+  // slot never enters.
+  const int srow = lane >> 4, spc = lane & 15;
+  const unsigned lds_k = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.k[0][0][0];
+  const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
+  auto issue_kv = [&](int blk, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int key = blk * AKB + (tid >> 4) + 32 * i;
-      const long long off = (long long)(key < kmax ? key : 0) * AD + sc * 8;
-      kst[i] = *reinterpret_cast<const pv4*>(kbase + off);
-      vst[i] = *reinterpret_cast<const pv4*>(vbase + off);
-    }
-  };
-  auto store_kv = [&](int buf, int blk) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int kr = (tid >> 4) + 32 * i;
-      const bool live = blk * AKB + kr < kmax;
-      *reinterpret_cast<pv4*>(&sm.kv.k[buf][kr][sc * 8]) = kst[i];
-      *reinterpret_cast<pv4*>(&sm.kv.v[buf][kr][sc * 8]) = live ? vst[i] : pv4{0u, 0u, 0u, 0u};
+      const int r = 4 * (2 * wave + i) + srow;   // row of the block
+      const int key = blk * AKB + r;
+      const long long row = (long long)(key < kmax ? key : 0) * AD;
+      const int kc = spc ^ (r & 15);                                   // logical K chunk
+      const int vc = 2 * ((spc >> 1) ^ (r & 7)) + (spc & 1);           // logical V chunk
+      const unsigned off = (unsigned)((buf * AKB + 4 * (2 * wave + i)) * 256);
+      lds_dma16(kbase + row + kc * 8, lds_k + off);
+      lds_dma16(vbase + row + vc * 8, lds_v + off);
     }
   };
 
@@ -707,13 +719,12 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
 #pragma unroll
     for (int nd = 0; nd < 8; ++nd) o[mt][nd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  load_kv(0);
-  store_kv(0, 0);
+  issue_kv(0, 0);
+  lds_dma_wait();
   __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
-    const int nb = blk + 1 < nblk ? blk + 1 : blk;
-    load_kv(nb);
     const int buf = blk & 1;
+    if (blk + 1 < nblk) issue_kv(blk + 1, buf ^ 1);  // that buffer was last read one block ago
     const int kb0 = blk * AKB;
     // S^T for 4 tiles of 16 keys: A = K rows 16 nt + r, dims 32 kt + 8 q (one LDS read per
     // (nt, kt), both query tiles)
@@ -724,7 +735,7 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
       st[1][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(&sm.kv.k[buf][16 * nt + rr][32 * kt + 8 * qq]);
+        const uint4 kf = __builtin_bit_cast(uint4, sm.kv.k[buf][16 * nt + rr][(4 * kt + qq) ^ rr]);
         st[0][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), qb8[0][kt], st[0][nt], 0, 0, 0);
         st[1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), qb8[1][kt], st[1][nt], 0, 0, 0);
       }
@@ -776,20 +787,22 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
     // V[32 kk + 4 q + s / 4 (+16)][16 nd + 4 (s % 4)]), one read pair per (kk, nd) for both tiles
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const bf16_t* vs = &sm.kv.v[buf][32 * kk + 4 * qq + (rr >> 2)][4 * (rr & 3)];
+      // row 32 kk + 4 q + r / 4 (+ 16), 8 bytes at column 16 nd + 4 (r % 4) of its swizzled block
+      const int vr = 32 * kk + 4 * qq + (rr >> 2);
+      const bf16_t* vlo = reinterpret_cast<const bf16_t*>(&sm.kv.v[buf][vr][0]) + 4 * (rr & 3);
+      const bf16_t* vhi = reinterpret_cast<const bf16_t*>(&sm.kv.v[buf][vr + 16][0]) + 4 * (rr & 3);
 #pragma unroll
       for (int nd = 0; nd < 8; ++nd) {
-        const av4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 16 * nd));
-        const av4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vs + 16 * AVROW + 16 * nd));
+        const av4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vlo + 16 * (nd ^ (vr & 7))));
+        const av4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_av4i16*)(vhi + 16 * (nd ^ ((vr + 16) & 7))));
         const uint4 vv = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                     __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
         o[0][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), as_bf16x8(pb[0][kk]), o[0][nd], 0, 0, 0);
         o[1][nd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), as_bf16x8(pb[1][kk]), o[1][nd], 0, 0, 0);
       }
     }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    store_kv(buf ^ 1, nb);  // buffer last read one iteration ago (behind the barrier below)
-    __syncthreads();
+    lds_dma_wait();  // this wavefront's next-block loads have landed ...
+    __syncthreads();  // ... and, past the barrier, every wavefront's
   }
 
   // ---- normalise and write: rows 16 mt + r (query r of tile mt) x 128 dims through LDS (bf16,
@@ -877,7 +890,7 @@ int qwen_attn_prefill(const void* q, const void* k_cache, const void* v_cache, v
   p.scale = scale;
   const long long blocks = p.bh_count * p.qblocks;
   if (blocks > 0x7fffffffLL) return QWEN_EARG;
-  if (wide) pf_attn_wide_kernel<<<dim3((unsigned)blocks), AW2 * 64, 0, stream>>>(p);
+  if (wide) pf_attn_wide_kernel<<<dim3((unsigned)((blocks + 7) / 8 * 8)), AW2 * 64, 0, stream>>>(p);  // 8 equal runs
   else pf_attn_kernel<<<dim3((unsigned)blocks), 256, 0, stream>>>(p);
   QWEN_RETURN_LAUNCH();
 }
