@@ -698,17 +698,17 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
   const int srow = lane >> 4, spc = lane & 15;
   const unsigned lds_k = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.k[0][0][0];
   const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
-  auto issue_kv = [&](int blk, int buf) __attribute__((always_inline)) {
+  // (K and V are issued separately, so a block's four loads per wavefront do not go out in one
+  // burst)
+  auto issue_kv = [&](int blk, int buf, bool k) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 4 * (2 * wave + i) + srow;   // row of the block
       const int key = blk * AKB + r;
       const long long row = (long long)(key < kmax ? key : 0) * AD;
-      const int kc = spc ^ (r & 15);                                   // logical K chunk
-      const int vc = 2 * ((spc >> 1) ^ (r & 7)) + (spc & 1);           // logical V chunk
       const unsigned off = (unsigned)((buf * AKB + 4 * (2 * wave + i)) * 256);
-      lds_dma16(kbase + row + kc * 8, lds_k + off);
-      lds_dma16(vbase + row + vc * 8, lds_v + off);
+      if (k) lds_dma16(kbase + row + (spc ^ (r & 15)) * 8, lds_k + off);            // logical K chunk
+      else lds_dma16(vbase + row + (2 * ((spc >> 1) ^ (r & 7)) + (spc & 1)) * 8, lds_v + off);  // V chunk
     }
   };
 
@@ -719,12 +719,14 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
 #pragma unroll
     for (int nd = 0; nd < 8; ++nd) o[mt][nd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  issue_kv(0, 0);
+  issue_kv(0, 0, true);
+  issue_kv(0, 0, false);
   lds_dma_wait();
   __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
     const int buf = blk & 1;
-    if (blk + 1 < nblk) issue_kv(blk + 1, buf ^ 1);  // that buffer was last read one block ago
+    const bool more = blk + 1 < nblk;
+    if (more) issue_kv(blk + 1, buf ^ 1, true);  // that buffer was last read one block ago
     const int kb0 = blk * AKB;
     // S^T for 4 tiles of 16 keys: A = K rows 16 nt + r, dims 32 kt + 8 q (one LDS read per
     // (nt, kt), both query tiles)
@@ -740,6 +742,7 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
         st[1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), qb8[1][kt], st[1][nt], 0, 0, 0);
       }
     }
+    if (more) issue_kv(blk + 1, buf ^ 1, false);
     if (kb0 + AKB - 1 > wave_first) {  // block reaches past some query's last key: mask
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
