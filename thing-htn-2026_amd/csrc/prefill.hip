@@ -197,14 +197,16 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(PfGemmParams p) {
 }
 
 
-// Wide form of the prompt GEMM (qwen_gemm for N a multiple of 256): a workgroup of 4
-// wavefronts computes a 256-row x 256-column tile, wavefront (wm, wn) a 128 x 128 quadrant
-// (8 x 8 accumulator tiles, 256 registers: they live in the AGPRs, one wavefront per SIMD).
-// Both operands are staged in LDS per k-step of 64 (double buffered, 2 x 64 KB): A rows as in
-// pf_gemm_kernel (16-byte chunk c of row r at slot c ^ (r % 8)), W as its 1 KB MFMA tiles in
-// their global order. Per k-step and CU that is 64 KB from L2 for 8.4 MFLOP, half of
-// pf_gemm_kernel's traffic per flop, and 128 KB of LDS fragment reads against 2048 MFMA cycles
-// per SIMD. The product is computed transposed, D^T = W X^T: a weight tile is the MFMA's A
+// Wide form of the prompt GEMM (qwen_gemm for N a multiple of 256): a workgroup of WV
+// wavefronts computes a 256-row x 256-column tile, wavefront (wm, wn) a 128-row x 512 / WV-column
+// part (8 x 32 / WV accumulator tiles). With WV = 8 (the launched form) that is 128 registers
+// of accumulators and two wavefronts per SIMD, so one wavefront's LDS reads and load issues
+// run under the other's MFMAs (measured against WV = 4, 128 x 128 parts in the AGPRs and one
+// wavefront per SIMD: gate/up 1137 -> 1176, down 1031 -> 1092, QKV 1069 -> 1053, O 1044 -> 1018
+// TFLOP/s). Both operands are staged in LDS per k-step of 64 (double buffered, 2 x 64 KB): A rows
+// as in pf_gemm_kernel (16-byte chunk c of row r at slot c ^ (r % 8)), W as its 1 KB MFMA tiles
+// in their global order. Per k-step and CU that is 64 KB from L2 for 8.4 MFLOP, half of
+// pf_gemm_kernel's traffic per flop. The product is computed transposed, D^T = W X^T: a weight tile is the MFMA's A
 // operand as it stands (lane (q, r): row r, k 8 q ..) and an A-row fragment its B operand, so
 // lane (q, r) of accumulator tile (mb, nb) holds D[16 mb + r][16 nb + 4 q + i], four adjacent
 // output columns of one row: the epilogue writes them as one 8-byte store (SwiGLU pairs the
@@ -227,9 +229,12 @@ __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0
 constexpr int PWM = 256;   // rows per workgroup
 constexpr int PWN = 256;   // weight rows (output columns before SwiGLU) per workgroup
 constexpr int PWG = 4;     // row tiles per group of the wide kernel's tile walk
+constexpr int PWV = 8;     // wavefronts of the wide kernel (two per SIMD, 128 x 64 quadrants each)
 
-template <int EPI>
-__global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
+template <int EPI, int WV>
+__global__ void __launch_bounds__(64 * WV, 1) pf_gemm_wide_kernel(PfGemmParams p) {
+  constexpr int NB = 32 / WV;        // 16-column accumulator tiles per wavefront (8 or 4)
+  constexpr int PAIRS = 32 / WV;     // (A block, W tile) direct loads per wavefront and stage
   __shared__ pv4 lds[2 * (PWM + PWN) * (PBK / 8)];  // [stage][A: 256 rows x 8 chunks | W: 32 tiles x 64 lanes]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -270,24 +275,24 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
   // Addresses are formed per load from the tile's origin (m0, nt0), both wavefront-uniform:
   // arrays of per-tile offsets kept across the tile loop would live in scratch memory.
   const int achunk = ((lane & 7) ^ (lane >> 3)) * 8;
-  const int arow = wave * 64 + (lane >> 3);  // + 8 i: this lane's row of A block 8 wave + i
+  const int arow = wave * PAIRS * 8 + (lane >> 3);  // + 8 i: this lane's row of A block PAIRS wave + i
   const pv4* wlane = reinterpret_cast<const pv4*>(p.w) + lane;
   // LDS byte address of stage 0 (stage 1 follows it)
   const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)lds;
-  // Loads i of a stage (i = 0 .. 7): the wavefront's A block 8 wave + i and W tile 8 wave + i.
+  // Loads i of a stage (i < PAIRS): the wavefront's A block PAIRS wave + i and W tile PAIRS wave + i.
   auto issue_pair = [&](long long m0, int nt0, int kb, int buf, int i) __attribute__((always_inline)) {
     const unsigned sb = lds0 + buf * ((PWM + PWN) * 8 * 16);
     const long long row = min(m0 + arow + 8 * i, (long long)p.M - 1);
-    lds_dma16(p.a + (int)row * p.K + achunk + kb * PBK, sb + (wave * 8 + i) * 1024);
-    const int t = wave * 8 + i;
+    lds_dma16(p.a + (int)row * p.K + achunk + kb * PBK, sb + (wave * PAIRS + i) * 1024);
+    const int t = wave * PAIRS + i;
     lds_dma16(wlane + ((long long)(nt0 + (t >> 1)) * KT + kb * 2 + (t & 1)) * 64, sb + (PWM * 8 + t * 64) * 16);
   };
   auto issue = [&](long long m0, int nt0, int kb, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) issue_pair(m0, nt0, kb, buf, i);
+    for (int i = 0; i < PAIRS; ++i) issue_pair(m0, nt0, kb, buf, i);
   };
 
-  f32x4_t acc[8][8];
+  f32x4_t acc[8][NB];
 
   // One k-step on stage `buf`: the first half k-step's 16 fragments (8 W, 8 A-row) are read,
   // then the half's MFMAs run in groups of 8 (one A-row fragment each). After each group two of
@@ -299,31 +304,31 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
   // under the MFMAs. The scheduling barriers pin that order.
   auto kstep = [&](int buf, bool nload, long long nm0, int nnt0, int nkb) __attribute__((always_inline)) {
     const pv4* cur = lds + buf * ((PWM + PWN) * 8);
-    auto wfrag = [&](int kt, int nb) { return __builtin_bit_cast(bf16x8_t, cur[PWM * 8 + ((wn * 8 + nb) * 2 + kt) * 64 + lane]); };
+    auto wfrag = [&](int kt, int nb) { return __builtin_bit_cast(bf16x8_t, cur[PWM * 8 + ((wn * NB + nb) * 2 + kt) * 64 + lane]); };
     auto xfrag = [&](int kt, int mb) {
       const int row = wm * 128 + mb * 16 + rr;
       return __builtin_bit_cast(bf16x8_t, cur[row * 8 + ((kt * 4 + qq) ^ (row & 7))]);
     };
-    bf16x8_t w0[8], x0[8], w1[8], x1[8];
+    bf16x8_t w0[NB], x0[8], w1[NB], x1[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w0[j] = wfrag(0, j);
+    for (int j = 0; j < NB; ++j) w0[j] = wfrag(0, j);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x0[j] = xfrag(0, j);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[nb], x0[mb], acc[mb][nb], 0, 0, 0);
-      w1[mb] = wfrag(1, mb);
+      if (mb < NB) w1[mb] = wfrag(1, mb);
       x1[mb] = xfrag(1, mb);
-      if (nload) issue_pair(nm0, nnt0, nkb, buf ^ 1, mb);
+      if (nload && mb < PAIRS) issue_pair(nm0, nnt0, nkb, buf ^ 1, mb);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[nb], x1[mb], acc[mb][nb], 0, 0, 0);
     }
     // The MFMAs only touch registers, so the scheduler may sink them below the barrier and the
@@ -343,7 +348,7 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
       if (grow >= p.M) continue;
       if constexpr (EPI == PEPI_SWIGLU) {
   #pragma unroll
-        for (int pj = 0; pj < 4; ++pj) {
+        for (int pj = 0; pj < NB / 2; ++pj) {
           float o[4];
   #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -352,13 +357,13 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
             const float sg = rbf(g / (1.0f + expf(-g)));
             o[i] = mul_rn(sg, u);
           }
-          const long long col = (long long)(nt0 / 2 + wn * 4 + pj) * 16 + 4 * qq;
+          const long long col = (long long)(nt0 / 2 + wn * (NB / 2) + pj) * 16 + 4 * qq;
           *reinterpret_cast<uint2*>(p.out + grow * p.ldo + col) = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
         }
       } else {
   #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-          const long long col = (long long)(nt0 + wn * 8 + nb) * 16 + 4 * qq;
+        for (int nb = 0; nb < NB; ++nb) {
+          const long long col = (long long)(nt0 + wn * NB + nb) * 16 + 4 * qq;
           float o[4];
   #pragma unroll
           for (int i = 0; i < 4; ++i) o[i] = acc[mb][nb][i];
@@ -391,7 +396,7 @@ __global__ void __launch_bounds__(256, 1) pf_gemm_wide_kernel(PfGemmParams p) {
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb + 1 < KB; ++kb) {  // the next stage is this tile's k-step kb + 1
       kstep(buf, true, m0, nt0, kb + 1);
       buf ^= 1;
@@ -864,9 +869,9 @@ int qwen_gemm(const void* a, const void* w_tiled, void* out, int M, int N, int K
   }
   const dim3 grid((unsigned)blocks);
   if (wide) {
-    if (epi == PEPI_STORE) pf_gemm_wide_kernel<PEPI_STORE><<<grid, 256, 0, stream>>>(p);
-    else if (epi == PEPI_RES) pf_gemm_wide_kernel<PEPI_RES><<<grid, 256, 0, stream>>>(p);
-    else pf_gemm_wide_kernel<PEPI_SWIGLU><<<grid, 256, 0, stream>>>(p);
+    if (epi == PEPI_STORE) pf_gemm_wide_kernel<PEPI_STORE, PWV><<<grid, 64 * PWV, 0, stream>>>(p);
+    else if (epi == PEPI_RES) pf_gemm_wide_kernel<PEPI_RES, PWV><<<grid, 64 * PWV, 0, stream>>>(p);
+    else pf_gemm_wide_kernel<PEPI_SWIGLU, PWV><<<grid, 64 * PWV, 0, stream>>>(p);
     QWEN_RETURN_LAUNCH();
   }
   if (epi == PEPI_STORE) pf_gemm_kernel<PEPI_STORE><<<grid, 256, 0, stream>>>(p);
