@@ -45,7 +45,8 @@ int qwen_silu_mul(const void* gu, void* out, int M, int I, hipStream_t stream);
 /* qk_norm_rope_cache(qkv [B*T, (Nq+2Nkv)*D], q_norm_w [D], k_norm_w [D], eps, cos/sin [P, D],
  * positions [B] int32, T, k_cache/v_cache [B, Nkv, CAP, D]) -> q_out [B, T, Nq, D];
  * writes K (normed + RoPE) and V at slots positions[b] + t (P = rows of the cos/sin tables;
- * a slot outside [0, min(CAP, P)) is skipped, never written). D must be 128.
+ * a slot outside [0, min(CAP, P)) is skipped, never written). D must be 128, and every
+ * tensor pointer 16-byte aligned (QWEN_EARG otherwise).
  * Replaces engine/kernels/rope.py:169-226 (qk_norm_rope_cache) / torch_ref.py:107-162. */
 int qwen_qk_norm_rope_cache(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
                             const void* sin_tab, const int32_t* positions, void* q_out, void* k_cache, void* v_cache,
