@@ -25,7 +25,8 @@ launch over the measured launch time, against the 2.5 PFLOP/s bf16 dense peak); 
 HBM-bound, so this is a secondary figure. ``cpu_baseline``: the oracle's torch-CPU decode step
 over all 36 layers on this host's cores, median of 3 runs (a bounded sample of the c2 decode).
 
-``--config c3|c4`` run one decode config; ``--config c5`` replays the speculative verify graph
+``--config c3|c4`` run one decode config (``roofline``: gate/up at c3, attention at c4, each
+that step's largest kernel); ``--config c5`` replays the speculative verify graph
 (B = 4, T = 5, context 4096) and reports verify steps/s. ``--profile-sample`` runs only the
 dominant kernel (and a copy of known size) for rocprofv3 counter runs.
 """
@@ -440,7 +441,12 @@ def main():
     B, S, N = CONFIGS[first]
     K = args.steps if args.steps is not None else N - 1 - W
     res = run_decode(eng, torch, cfg, B, S, N, K, W)
-    avg, nbytes, name = time_gate_up(eng, torch)
+    if first == "c4":  # the KV-bound step: attention is 68 % of its kernel time
+        avg, nbytes, name = time_attention(eng, torch)
+        what = "QK-norm + RoPE + KV write + GQA attention (one layer)"
+    else:
+        avg, nbytes, name = time_gate_up(eng, torch)
+        what = "RMSNorm + gate/up + SwiGLU (one layer)"
     out = {
         "metric": ("decode tok/s at B=1 and B=32 (Qwen3-4B bf16); HBM GB/s as % of peak" if args.config == "default"
                    else f"decode tok/s at B={B} (Qwen3-4B bf16)"),
@@ -449,7 +455,7 @@ def main():
         "dtype": "bf16", "data": DATA,
         "config": {"workload": f"{first}: Qwen3-4B, B={B}, prompt {S}, {N} greedy decode steps",
                    "global_batch": B, "seq_len": S, "decode_steps": N, "parallelism": "single GPU"},
-        "roofline": roofline(avg, nbytes, name, first, "RMSNorm + gate/up + SwiGLU (one layer)"),
+        "roofline": roofline(avg, nbytes, name, first, what),
         "step_roofline": res["step_roofline"],
         "ttft_s": res["ttft_s"],
         "steps_note": ("steps = decode steps launched inside the timed window; the engine queues up to "
