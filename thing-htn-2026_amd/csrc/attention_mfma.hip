@@ -75,31 +75,7 @@ __device__ __forceinline__ void mload2_dev(const float* q, float& a, float& b) {
   b = __uint_as_float((unsigned)(v >> 32));
 }
 
-// Max over the 16 lanes of a DPP row (lanes 16 g .. 16 g + 15) on lane permutations, with no
-// LDS round trip: quad xor 1, quad xor 2 (quad maxima), half-row mirror (lane i <- 7 - i of its
-// 8: the two quads), row mirror (lane i <- 15 - i: the two halves). Max is exact, so the order
-// does not change the result.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-// Sum over the 16 lanes of a DPP row with the same permutations. After the two quad steps all
-// lanes of a quad hold the same value, so the mirrors add the same operands as lane ^ 4 and
-// lane ^ 8 would: the result equals the xor-butterfly sum bit for bit.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x141>(v);
-  v += dpp_mov<0x140>(v);
-  return v;
-}
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
-  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
-  return v;
-}
+// Row reductions (row16_sum, row16_max: 16-lane DPP rows, no LDS round trip) are in common.h.
 
 // One 128-wide head held as dims (c, c + 64) by lane c of a wavefront (x0, x1), with the
 // gain (g0, g1) and the cos / sin table entries of its position already loaded: RMSNorm

@@ -100,11 +100,47 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_mov_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float wave_sum_dpp(float v) {
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+// Sum over the 16 lanes of each DPP row (lanes 16 g .. 16 g + 15); every lane of the row ends
+// with the sum. After the two quad steps all lanes of a quad hold the same value, so the
+// mirrors add the same operands as lane ^ 4 and lane ^ 8 would: the result equals the xor
+// butterfly (1, 2, 4, 8) bit for bit. Every lane of the wavefront must be active.
+__device__ __forceinline__ float row16_sum(float v) {
   v += dpp_mov_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
   v += dpp_mov_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
   v += dpp_mov_f<0x141>(v);  // row_half_mirror
   v += dpp_mov_f<0x140>(v);  // row_mirror
+  return v;
+}
+// Maximum over the 16 lanes of each DPP row on the same permutations (max is exact, so the
+// order does not change the result).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov_f<0xB1>(v));
+  v = fmaxf(v, dpp_mov_f<0x4E>(v));
+  v = fmaxf(v, dpp_mov_f<0x141>(v));
+  v = fmaxf(v, dpp_mov_f<0x140>(v));
+  return v;
+}
+// (largest value, lowest index among equals) over the 16 lanes of each DPP row, on the same
+// permutations; every lane of the row ends with the result. The combine is symmetric and
+// associative for finite values, so the result does not depend on the order of the steps.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& best, int& bidx) {
+  const float ov = dpp_mov_f<CTRL>(best);
+  const int oi = dpp_mov_i<CTRL>(bidx);
+  if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+}
+__device__ __forceinline__ void row16_argmax(float& best, int& bidx) {
+  argmax_dpp_step<0xB1>(best, bidx);
+  argmax_dpp_step<0x4E>(best, bidx);
+  argmax_dpp_step<0x141>(best, bidx);
+  argmax_dpp_step<0x140>(best, bidx);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = row16_sum(v);
   const int b = __builtin_bit_cast(int, v);
   const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
   const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));

@@ -300,12 +300,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
           const int col = (int)(unit * NTW + nt) * 16 + r;
           if (v > best) { best = v; bidx = col; }
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-          const float ov = __shfl_xor(best, o, 64);
-          const int oi = __shfl_xor(bidx, o, 64);
-          if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
-        }
+        row16_argmax(best, bidx);  // over the 16 columns r of this row
         if (r == 0 && mok) {
           const unsigned long long key =
               ((unsigned long long)ordered_bits(best) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)bidx);
@@ -331,11 +326,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x4_t (&acc)[MT]
               if (mok) orow[col] = o;
               if (p.psq_out) {  // partial sum of squares of the new row over these 16 columns
                 const float v = bf2f(o);
-                float sq = mul_rn(v, v);
-                sq += __shfl_xor(sq, 1, 64);
-                sq += __shfl_xor(sq, 2, 64);
-                sq += __shfl_xor(sq, 4, 64);
-                sq += __shfl_xor(sq, 8, 64);
+                const float sq = row16_sum(mul_rn(v, v));
                 if (mok && r == 0) p.psq_out[(size_t)m * (p.N >> 4) + (col >> 4)] = sq;
               }
             } else {

@@ -438,25 +438,6 @@ struct PfAttnSmem {
   bf16_t pm[4][16][AKB];
 };
 
-template <int CTRL>
-__device__ __forceinline__ float pdpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float prow16_max(float v) {
-  v = fmaxf(v, pdpp<0xB1>(v));
-  v = fmaxf(v, pdpp<0x4E>(v));
-  v = fmaxf(v, pdpp<0x141>(v));
-  v = fmaxf(v, pdpp<0x140>(v));
-  return v;
-}
-__device__ __forceinline__ float prow16_sum(float v) {
-  v += pdpp<0xB1>(v);
-  v += pdpp<0x4E>(v);
-  v += pdpp<0x141>(v);
-  v += pdpp<0x140>(v);
-  return v;
-}
-
 __global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
   __shared__ PfAttnSmem sm;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -550,7 +531,7 @@ __global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
         sv[nt] = vis ? s[nt][i] * p.scale : ANEG;
         mx = fmaxf(mx, sv[nt]);
       }
-      mx = prow16_max(mx);
+      mx = row16_max(mx);
       const float mn = fmaxf(m[i], mx);
       alpha[i] = __expf(m[i] - mn);
       float psum = 0.f;
@@ -593,7 +574,7 @@ __global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
 
   // ---- normalise and write: the wavefront's 16 rows x 128 dims through LDS (bf16), 16-byte stores
 #pragma unroll
-  for (int i = 0; i < 4; ++i) l[i] = prow16_sum(l[i]);
+  for (int i = 0; i < 4; ++i) l[i] = row16_sum(l[i]);
   bf16_t* ot = &sm.k[0][0][0] + wave * 16 * AKROW;  // 16 rows of 272 B per wavefront
 #pragma unroll
   for (int nd = 0; nd < 8; ++nd)
