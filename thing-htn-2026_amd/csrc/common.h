@@ -139,6 +139,27 @@ __device__ __forceinline__ void row16_argmax(float& best, int& bidx) {
   argmax_dpp_step<0x141>(best, bidx);
   argmax_dpp_step<0x140>(best, bidx);
 }
+// Combine lane l with lane l ^ 16 (rows 2g and 2g + 1) or l ^ 32 (the two halves) on the
+// gfx950 lane-swap instructions (v_permlane16_swap / v_permlane32_swap: VALU, no LDS round
+// trip). Called with the same value twice, the swap leaves the two lanes' values in the two
+// results, so their sum (or maximum) equals v + __shfl_xor(v, 16 / 32) bit for bit (the
+// addition is commutative). The compiler inserts the instructions' wait states.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = row16_sum(v);
   const int b = __builtin_bit_cast(int, v);

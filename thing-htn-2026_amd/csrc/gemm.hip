@@ -146,8 +146,7 @@ struct AOperand {
             for (int u = 4 * per; u < nu; ++u) s += q == 3 ? ps[u] : 0.f;
           }
         }
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
+        s = xor32_sum(xor16_sum(s));  // the row's four quarters (lanes r, r + 16, r + 32, r + 48)
         rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
       }
     }
@@ -368,7 +367,7 @@ __device__ __forceinline__ void finish_split(const GemmParams& p, f32x4_t (&acc)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   unsigned old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(p.cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __shfl(old, 0, 64);
+  old = __builtin_amdgcn_readfirstlane(old);  // lane 0's (every lane is active here)
   if (old != (unsigned)(pieces - 1)) return;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   // Pieces are requested FS_BATCH at a time (one round trip per batch rather than per

@@ -615,14 +615,8 @@ constexpr int AQ2 = AW2 * 2 * 4;     // query tokens per workgroup (2 tiles of 4
 // with scale folded in; rounding points as pf_attn_kernel (P rounded to bf16 for PV, l from the
 // unrounded P, O normalised in fp32, then rounded). exp2 is the hardware v_exp_f32: a P below
 // 2^-126 of the block maximum flushes to 0, far under bf16's resolution of the row sum.
-__device__ __forceinline__ float xlane_max4(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float xlane_sum4(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
-}
+__device__ __forceinline__ float xlane_max4(float v) { return xor32_max(xor16_max(v)); }
+__device__ __forceinline__ float xlane_sum4(float v) { return xor32_sum(xor16_sum(v)); }
 
 __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams p) {
   // K / V blocks in 256-byte rows with no padding (direct-to-LDS loads fill 1 KB runs), swizzled
