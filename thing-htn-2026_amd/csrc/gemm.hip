@@ -580,16 +580,18 @@ __global__ void __launch_bounds__(64 * SK_WAVES) sk_gemm_kernel(GemmParams p) {
 // Staging is one straight-line round: wavefront w stages rows w and w + WPG
 // (each lane up to RECT_CPL 16-byte chunks per row) and, with NORM, derives those
 // rows' RMSNorm factors itself from the producer's per-16-column partial sums, so
-// no barrier separates statistics and staging. Its loads are issued before the
-// first weight batches, so the staging wait is one activation round trip while
-// the weights are already in flight. Staged rows hold only the M real rows (no
-// padding): 16-byte chunk j of row m sits at chunk j ^ (m % 16) of its row, which
-// keeps both the staging writes and the A-fragment reads (16 rows x one chunk
-// each) free of bank conflicts; rows past M read as zero.
+// no barrier separates statistics and staging. The first weight batches are
+// requested once the staged rows are stored (loads return in issue order, so
+// earlier weight requests would hold the staging behind HBM). Staged rows hold the
+// M real rows plus, when the 16-row tiles have padding rows, one zero row that
+// those rows read: 16-byte chunk j of row m sits at chunk j ^ (m % 16) of its row,
+// which keeps both the staging writes and the A-fragment reads (16 rows x one
+// chunk each) free of bank conflicts.
 //
 // A piece is at most one unit long (the host checks units per rectangle <= WPG),
 // so it touches at most two units: the first unit's sums are parked in registers
-// when the second starts. Wavefront partials meet in LDS in wavefront order; with
+// when the second starts, at a tile index every lane of the wavefront knows, so
+// the loop has no per-lane selects. Wavefront partials meet in LDS in wavefront order; with
 // GK > 1 the GK rectangles of one unit column meet in finish_split (pieces in k
 // order).
 constexpr int RECT_LDS_MAX = 160 * 1024;
@@ -614,24 +616,28 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
   const int rowe = kc * 32;  // bf16 per staged row
   bf16_t* xs = reinterpret_cast<bf16_t*>(rect_smem);
 
-  // Tile (unit u, k-step k) of this rectangle: u in [0, nun), k in [0, kc).
+  // The wavefront's piece: n tiles of the (unit, k-step) plane in unit-major order, at most one
+  // unit long. Its tiles 0 .. tb - 1 are k-steps kfirst .. of unit ufirst, tiles tb .. n - 1 are
+  // k-steps 0 .. of unit ufirst + 1. Every quantity here is wavefront-uniform, so the tile
+  // addresses are scalar; an empty piece points at the rectangle's first tile.
   const uint4* wt = reinterpret_cast<const uint4*>(p.w);
-  auto tile_ptr = [&](int u, int k, int nt) { return wt + ((size_t)(u0 + u) * NTW + nt) * KT * 64 + (size_t)(k0 + k) * 64 + lane; };
-  struct Batch {
-    uint4 bt[U][NTW];
+  const int n = t1 - t0;
+  const int ufirst = n > 0 ? t0 / kc : 0;
+  const int kfirst = n > 0 ? t0 - ufirst * kc : 0;
+  const int tb = min(n, kc - kfirst);
+  const size_t ustride = (size_t)NTW * KT * 64;  // 16-byte pieces per unit of the tiled weight
+  const uint4* wA = wt + (size_t)(u0 + ufirst) * ustride + (size_t)(k0 + kfirst) * 64;
+  const uint4* wB = wt + (size_t)min(u0 + ufirst + 1, NU - 1) * ustride + (size_t)k0 * 64;
+  // Tile t of the piece; a tile at or past n (a partly used last batch) re-reads tile 0.
+  auto tile_base = [&](int t) -> const uint4* {
+    return t < tb ? wA + (size_t)t * 64 : (t < n ? wB + (size_t)(t - tb) * 64 : wA);
   };
-  // The wavefront's first tile (a valid tile whenever its piece is not empty).
-  const int ufirst = t0 / kc, kfirst = t0 - (t0 / kc) * kc;
-  // Issue the U tiles starting at cursor (cu, ck), the position of tile t; tiles at or past
-  // t1 re-read the rectangle's first tile (always valid; dead tiles meet a zero A operand).
-  auto issue = [&](Batch& b, int t, int cu, int ck) {
+  auto issue = [&](uint4 (&w)[U][NTW], int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      int uu = cu, kk = ck + i;
-      if (kk >= kc) { kk -= kc; ++uu; }
-      if (t + i >= t1) { uu = 0; kk = 0; }
+      const uint4* b = tile_base(t + i);
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) b.bt[i][nt] = load_nt(tile_ptr(uu, kk, nt));
+      for (int nt = 0; nt < NTW; ++nt) w[i][nt] = load_nt(b + (size_t)nt * KT * 64 + lane);
     }
   };
 
@@ -664,13 +670,8 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
     }
   }
 
-  const int nb = (t1 - t0 + U - 1) / U;
-  Batch b0, b1;
-  int ic_u = ufirst, ic_k = kfirst;  // issue cursor: tile t0 + U * (batches issued)
-  auto advance = [&](int& cu, int& ck) {
-    ck += U;
-    if (ck >= kc) { ck -= kc; ++cu; }
-  };
+  const int nb = (n + U - 1) / U;
+  uint4 b0[U][NTW], b1[U][NTW];
   // Normalise and store the staged rows (row m: RMSNorm factor from the K/16 partials,
   // summed lane-strided then by a fixed butterfly: identical in every workgroup). This
   // completes before the first weight batch is requested: loads return in issue order, so
@@ -704,25 +705,29 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
           *reinterpret_cast<uint4*>(xs + m * rowe + (j ^ (m & 15)) * 8) = v;
         }
       }
+    } else if (m == p.M && p.M < 16 * MT) {  // the zero row that A-fragment rows past M read
+#pragma unroll
+      for (int c = 0; c < RECT_CPL; ++c) {
+        const int j = lane + 64 * c;
+        if (j < cpr) *reinterpret_cast<uint4*>(xs + m * rowe + j * 8) = make_uint4(0, 0, 0, 0);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the weight requests below the staging
   // Both prologue batches unconditionally (an empty piece re-reads the rectangle's first
   // tile): every path then has the same loads in flight, so the compiler's wait for batch 0
   // leaves batch 1 in flight. They stream while the workgroup meets at the barrier.
-  issue(b0, t0, ic_u, ic_k);
-  advance(ic_u, ic_k);
-  issue(b1, t0 + U, ic_u, ic_k);
-  advance(ic_u, ic_k);
+  issue(b0, 0);
+  issue(b1, U);
   __syncthreads();
 
-  // A-fragment rows of this lane: rows past M read row 0's slot and are zeroed.
-  int arow[MT];
-  bool aok[MT];
+  // A-fragment rows of this lane: rows past M read the zero row (row M).
+  int abase[MT], asw[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    aok[mt] = 16 * mt + r < p.M;
-    arow[mt] = aok[mt] ? 16 * mt + r : 0;
+    const int arow = 16 * mt + r < p.M ? 16 * mt + r : p.M;
+    abase[mt] = arow * rowe;
+    asw[mt] = arow & 15;
   }
 
   f32x4_t acc[MT][NTW], saved[MT][NTW];
@@ -730,57 +735,50 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = saved[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  int cc_u = ufirst, cc_k = kfirst;  // consume cursor
-  int ucur = ufirst;                             // unit being accumulated (wave-uniform)
-  // Branch-free: a dead tile (past t1) meets a zero A operand, and the switch to the second
-  // unit parks the sums with selects.
-  auto consume = [&](const Batch& b, int t) {
+  // Tile t: the unit switch (t == tb: the first unit's sums are parked) and a tile past the
+  // piece (t >= n, skipped) are wavefront-uniform branches, so the sums see no selects.
+  auto consume = [&](const uint4 (&w)[U][NTW], int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      int uu = cc_u, kk = cc_k + i;
-      if (kk >= kc) { kk -= kc; ++uu; }
-      const bool live = t + i < t1;
-      const bool sw = live && uu != ucur;
-      ucur = sw ? uu : ucur;
-      kk = live ? kk : 0;
+      const int tt = t + i;
+      if (tt < n) {
+        if (tt == tb) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) {
-          saved[mt][nt] = sw ? acc[mt][nt] : saved[mt][nt];
-          acc[mt][nt] = sw ? f32x4_t{0.f, 0.f, 0.f, 0.f} : acc[mt][nt];
+            for (int nt = 0; nt < NTW; ++nt) {
+              saved[mt][nt] = acc[mt][nt];
+              acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
         }
+        const int kk = tt < tb ? kfirst + tt : tt - tb;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        uint4 araw = *reinterpret_cast<const uint4*>(xs + arow[mt] * rowe + (((kk * 4 + q) ^ (arow[mt] & 15)) * 8));
-        if (!live || !aok[mt]) araw = make_uint4(0, 0, 0, 0);
-        const bf16x8_t a = as_bf16x8(araw);
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8_t a = as_bf16x8(*reinterpret_cast<const uint4*>(xs + abase[mt] + (((kk * 4 + q) ^ asw[mt]) * 8)));
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b.bt[i][nt]), acc[mt][nt], 0, 0, 0);
+          for (int nt = 0; nt < NTW; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(w[i][nt]), acc[mt][nt], 0, 0, 0);
+        }
       }
     }
-    advance(cc_u, cc_k);
   };
   int j = 0;
   for (; j + 3 < nb; j += 2) {  // batches j .. j+3 exist
-    consume(b0, t0 + j * U);
-    issue(b0, t0 + (j + 2) * U, ic_u, ic_k);
-    advance(ic_u, ic_k);
-    consume(b1, t0 + (j + 1) * U);
-    issue(b1, t0 + (j + 3) * U, ic_u, ic_k);
-    advance(ic_u, ic_k);
+    consume(b0, j * U);
+    issue(b0, (j + 2) * U);
+    consume(b1, (j + 1) * U);
+    issue(b1, (j + 3) * U);
   }
-  if (j < nb) consume(b0, t0 + j * U);
-  if (j + 2 < nb) issue(b0, t0 + (j + 2) * U, ic_u, ic_k);
-  if (j + 1 < nb) consume(b1, t0 + (j + 1) * U);
-  if (j + 2 < nb) consume(b0, t0 + (j + 2) * U);
+  if (j < nb) consume(b0, j * U);
+  if (j + 2 < nb) issue(b0, (j + 2) * U);
+  if (j + 1 < nb) consume(b1, (j + 1) * U);
+  if (j + 2 < nb) consume(b0, (j + 2) * U);
 
   // Wavefront partials -> LDS ([wave][slot][mt][nt][lane], aliasing the staged A), then per unit.
   __syncthreads();
   f32x4_t* red = reinterpret_cast<f32x4_t*>(rect_smem);
-  if (t0 < t1) {
-    const bool two = (t1 - 1) / kc > ufirst;
+  if (n > 0) {
+    const bool two = tb < n;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -891,7 +889,8 @@ int dispatch(const GemmParams& p, int grid, int mt, int ntw, int wpg, hipStream_
 long long rect_lds_bytes(int M, int K, int ntw, int wpg, int gk) {
   const long long MT = M > 16 ? 2 : 1;
   const long long kc = (K / 32) / gk;
-  const long long xs = (long long)M * kc * 64;
+  const long long rows = M < 16 * MT ? M + 1 : M;  // plus the zero row when the tiles have padding rows
+  const long long xs = rows * kc * 64;
   const long long red = (long long)wpg * 2 * MT * ntw * 64 * 16;
   return xs > red ? xs : red;
 }

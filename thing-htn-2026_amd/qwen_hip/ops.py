@@ -490,7 +490,8 @@ def rect_fits(M: int, N: int, K: int, ntw: int, waves: int, gn: int, gk: int, no
     if kc * 4 > 64 * 5 or M > 2 * waves or (norm and K // 16 > 64 * 4) or -(-NU // gn) > waves:
         return False
     MT = 2 if M > 16 else 1
-    return max(M * kc * 64, waves * 2 * MT * ntw * 64 * 16) <= RECT_LDS_MAX
+    rows = M + 1 if M < 16 * MT else M   # the zero row that padding rows of the 16-row tiles read
+    return max(rows * kc * 64, waves * 2 * MT * ntw * 64 * 16) <= RECT_LDS_MAX
 
 
 def rect_config(M: int, N: int, K: int, silu_pair: bool = False, cus: int = 256, waves: int = 16,
