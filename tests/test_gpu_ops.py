@@ -78,7 +78,8 @@ def test_silu_mul(qops, rows, inter):
 
 @pytest.mark.parametrize("B,T,positions,NQ,NKV", [(2, 1, [5, 40], 8, 2), (2, 3, [0, 17], 8, 2),
                                                    (2, 9, [0, 0], 8, 2), (1, 1, [511], 32, 8),
-                                                   (4, 5, [4096, 100, 7, 2000], 32, 8)])
+                                                   (4, 5, [4096, 100, 7, 2000], 32, 8),
+                                                   (2, 300, [0, 3000], 32, 8)])   # a prompt chunk
 def test_qk_norm_rope_cache(qops, B, T, positions, NQ, NKV):
     g = torch.Generator().manual_seed(7)
     D, CAP = 128, 4160
@@ -101,6 +102,29 @@ def test_qk_norm_rope_cache(qops, B, T, positions, NQ, NKV):
         assert_close(got, want, 1e-2, 1 / 64, name)
         assert float((got != want).float().mean()) <= 1e-2, name
     assert torch.equal(vd.cpu(), vc_ref)    # V is copied raw; every other slot untouched
+
+
+def test_qk_norm_rope_cache_rejects_unaligned(qops):
+    """16-byte pieces: a view 2 bytes into its storage is refused by the wrapper and, called
+    directly, by the entry point (argument status, nothing launched)."""
+    from qwen_hip import _lib
+    D, CAP, B, T, NQ, NKV = 128, 64, 1, 1, 8, 2
+    cos, sin = R.rope_tables(128, 5e6, D)
+    qkv = torch.zeros(B * T * (NQ + 2 * NKV) * D + 1, dtype=BF16, device=DEV)
+    kc = torch.zeros(B, NKV, CAP, D, dtype=BF16, device=DEV)
+    vc = torch.zeros_like(kc)
+    g = torch.ones(D, dtype=BF16, device=DEV)
+    pos = torch.zeros(B, dtype=torch.int32, device=DEV)
+    bad = qkv[1:].view(B * T, (NQ + 2 * NKV) * D)
+    with pytest.raises(AssertionError, match="16-byte aligned"):
+        qops.qk_norm_rope_cache(bad, g, g, EPS, cos.to(DEV), sin.to(DEV), pos, T, kc, vc)
+    q = torch.empty(B, T, NQ, D, dtype=BF16, device=DEV)
+    with pytest.raises(RuntimeError, match="qwen_qk_norm_rope_cache"):
+        _lib.call("qwen_qk_norm_rope_cache", bad.data_ptr(), g.data_ptr(), g.data_ptr(), cos.to(DEV).data_ptr(),
+                  sin.to(DEV).data_ptr(), pos.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, T, NQ, NKV,
+                  D, CAP, 128, EPS, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert int(kc.count_nonzero()) == 0 and int(vc.count_nonzero()) == 0
 
 
 # ---------------------------------------------------------------- attention

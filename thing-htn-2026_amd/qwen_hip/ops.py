@@ -98,6 +98,8 @@ def qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions
     assert cos_tab.dtype == BF16 and sin_tab.dtype == BF16
     assert positions.dtype == torch.int32 and positions.numel() == B and positions.is_contiguous()
     q = out if out is not None else torch.empty((B, T, Nq, D), dtype=BF16, device=qkv.device)
+    for t in (qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, q, k_cache, v_cache):
+        assert t.data_ptr() % 16 == 0, "qk_norm_rope_cache reads and writes 16-byte pieces: tensors must be 16-byte aligned"
     _lib.call("qwen_qk_norm_rope_cache", qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
               cos_tab.data_ptr(), sin_tab.data_ptr(), positions.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
               v_cache.data_ptr(), B, T, Nq, Nkv, D, CAP, cos_tab.shape[0], float(eps), _stream())
