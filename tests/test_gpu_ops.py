@@ -416,6 +416,24 @@ def test_lm_head_argmax_one_hot_exact(qops):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("M", [4, 8, 20, 32])
+def test_lm_head_argmax_ties_within_a_tile(qops, M):
+    """All 16 columns of every 16-row weight tile are the same one-hot row, so each row of a
+    tile's logits is 16 equal values (and tiles t and t + K repeat them): the in-tile row
+    reduction must keep the lowest column, and the cross-tile keys the lowest tile."""
+    V, K = 4096, 256
+    g = torch.Generator().manual_seed(23 + M)
+    x = _bf16(M, K, gen=g)
+    nw = torch.ones(K, dtype=BF16)
+    w = torch.zeros(V, K, dtype=BF16)
+    w[torch.arange(V), (torch.arange(V) // 16) % K] = 1.0
+    logits = R.linear(R.rms_norm(x, nw, EPS), w)
+    want = logits.argmax(-1)
+    assert bool((want % 16 == 0).all())                 # torch's first-index rule: a tile's column 0
+    got = qops.lm_head_argmax(x.to(DEV), nw.to(DEV), EPS, qops.tile_weight(w.to(DEV))).cpu()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("M", [1, 4, 20, 32])
 def test_lm_head_argmax_random(qops, M):
     V, K = 151936, 2560
