@@ -92,10 +92,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Wave-wide sum without LDS round trips: each 16-lane row is summed on DPP lane permutations
-// (quad xor 1, quad xor 2, half-row mirror, row mirror: every lane of a row ends with the row
-// sum), then the four row sums are read out and added as (r0 + r1) + (r2 + r3). Fixed order
-// (deterministic); the result is uniform across the wavefront.
+// Lane permutations on DPP (VALU; no LDS round trip). The lanes a permutation reads from must
+// be active: the row reductions below read across whole 16-lane rows, the 8-lane reduction of
+// rope.hip within an 8-lane unit whose lanes return together.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
@@ -107,7 +106,7 @@ __device__ __forceinline__ int dpp_mov_i(int v) {
 // Sum over the 16 lanes of each DPP row (lanes 16 g .. 16 g + 15); every lane of the row ends
 // with the sum. After the two quad steps all lanes of a quad hold the same value, so the
 // mirrors add the same operands as lane ^ 4 and lane ^ 8 would: the result equals the xor
-// butterfly (1, 2, 4, 8) bit for bit. Every lane of the wavefront must be active.
+// butterfly (1, 2, 4, 8) bit for bit.
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_mov_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
   v += dpp_mov_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
@@ -160,6 +159,9 @@ __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// Wave-wide sum without LDS round trips: each 16-lane row is summed by row16_sum, then the
+// four row sums are read out and added as (r0 + r1) + (r2 + r3). Fixed order (deterministic);
+// the result is uniform across the wavefront.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = row16_sum(v);
   const int b = __builtin_bit_cast(int, v);
