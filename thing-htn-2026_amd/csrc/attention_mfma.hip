@@ -464,8 +464,39 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
     }
   __syncthreads();
 
-  // Thread -> (row, 8-dim chunk) items of the R x 128 result.
   constexpr int NT = 64 * WPG;
+  // One split and at most NT result elements (T = 1): one element per thread, so the whole
+  // workgroup shares the combine instead of one wavefront doing 8 elements per lane. Same
+  // operations in the same order per element as the loop below (bit-identical).
+  if (p.S == 1 && R * MD <= NT) {
+    const int it = threadIdx.x;
+    if (it < R * MD) {
+      const int row = it / MD, d = it - row * MD;
+      f32x2_t ml[WPG];
+      float ov[WPG];
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) {
+        const float* mrow = sm.u.merge[w][row];
+        ml[w] = *reinterpret_cast<const f32x2_t*>(mrow + MD);
+        ov[w] = mrow[d];
+      }
+      float M = MNEG;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) M = fmaxf(M, ml[w].x);
+      float L = 0.f, acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) {
+        const float sc = __expf(ml[w].x - M);
+        L += sc * ml[w].y;
+        acc += sc * ov[w];
+      }
+      const int t = row / MG, g = row - t * MG;
+      p.out[((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d] = f2bf(acc / L);
+    }
+    return;
+  }
+
+  // Thread -> (row, 8-dim chunk) items of the R x 128 result.
   const int items = R * (MD / 8);
   // Split partial of (bh, split): O [16 MT][MD] fp32 (16-byte aligned rows), then (m, l) per row.
   constexpr int PO = MT * 16 * MD, PSTRIDE = MT * 16 * (2 + MD);
