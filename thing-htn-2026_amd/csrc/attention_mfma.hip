@@ -465,10 +465,17 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   __syncthreads();
 
   constexpr int NT = 64 * WPG;
-  // One split and at most NT result elements (T = 1): one element per thread, so the whole
-  // workgroup shares the combine instead of one wavefront doing 8 elements per lane. Same
-  // operations in the same order per element as the loop below (bit-identical).
-  if (p.S == 1 && R * MD <= NT) {
+  // Thread -> (row, 8-dim chunk) items of the R x 128 result; with at most NT elements (T = 1),
+  // one element per thread, so the whole workgroup shares the combine instead of one wavefront
+  // doing 8 elements per lane (the same operations in the same order per element: the results
+  // are bit-identical).
+  const int items = R * (MD / 8);
+  const bool per_elem = R * MD <= NT;
+  // Split partial of (bh, split): O [16 MT][MD] fp32 (16-byte aligned rows), then (m, l) per row.
+  constexpr int PO = MT * 16 * MD, PSTRIDE = MT * 16 * (2 + MD);
+  float* mine = p.part + (bh * p.S + split) * PSTRIDE;
+  const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part + bh * p.S * PSTRIDE);
+  if (per_elem) {
     const int it = threadIdx.x;
     if (it < R * MD) {
       const int row = it / MD, d = it - row * MD;
@@ -490,19 +497,16 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
         L += sc * ml[w].y;
         acc += sc * ov[w];
       }
-      const int t = row / MG, g = row - t * MG;
-      p.out[((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d] = f2bf(acc / L);
+      if (p.S == 1) {
+        const int t = row / MG, g = row - t * MG;
+        p.out[((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d] = f2bf(acc / L);
+      } else {
+        if (d == 0) mstore2_dev(mine + PO + 2 * row, M, L);
+        store4_dev(prs, (split * PSTRIDE + row * MD + d) * 4, acc);
+      }
     }
-    return;
   }
-
-  // Thread -> (row, 8-dim chunk) items of the R x 128 result.
-  const int items = R * (MD / 8);
-  // Split partial of (bh, split): O [16 MT][MD] fp32 (16-byte aligned rows), then (m, l) per row.
-  constexpr int PO = MT * 16 * MD, PSTRIDE = MT * 16 * (2 + MD);
-  float* mine = p.part + (bh * p.S + split) * PSTRIDE;
-  const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part + bh * p.S * PSTRIDE);
-  for (int it = threadIdx.x; it < items; it += NT) {
+  for (int it = per_elem ? items : threadIdx.x; it < items; it += NT) {
     const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
     // every wavefront's (m, l) and 8 values requested at once (16-byte reads), then combined
     // in wavefront order
@@ -554,7 +558,36 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   __syncthreads();
   if (!sm.last) return;
   const float* all = p.part + bh * p.S * PSTRIDE;
-  for (int it = threadIdx.x; it < items; it += NT) {
+  if (per_elem) {
+    const int it = threadIdx.x;
+    if (it < R * MD) {
+      const int row = it / MD, d = it - row * MD;
+      // every split's (m, l) and value requested at once, merged in split order
+      float ms[MERGE_MAX], ls[MERGE_MAX], os[MERGE_MAX];
+#pragma unroll
+      for (int j = 0; j < MERGE_MAX; ++j) {
+        const int js = min(j, p.S - 1);
+        mload2_dev(all + js * PSTRIDE + PO + 2 * row, ms[j], ls[j]);
+        os[j] = load4_dev(prs, (js * PSTRIDE + row * MD + d) * 4);
+      }
+      float MM = MNEG;
+#pragma unroll
+      for (int j = 0; j < MERGE_MAX; ++j)
+        if (j < p.S) MM = fmaxf(MM, ms[j]);
+      float LL = 0.f, oo = 0.f;
+#pragma unroll
+      for (int j = 0; j < MERGE_MAX; ++j) {
+        if (j < p.S) {
+          const float sc = __expf(ms[j] - MM);
+          LL += sc * ls[j];
+          oo += sc * os[j];
+        }
+      }
+      const int t = row / MG, g = row - t * MG;
+      p.out[((b * T + t) * Nq + (long long)kvh * MG + g) * MD + d] = f2bf(oo / LL);
+    }
+  }
+  for (int it = per_elem ? items : threadIdx.x; it < items; it += NT) {
     const int row = it / (MD / 8), d0 = (it - row * (MD / 8)) * 8;
     // every split's partial requested at once (S <= MERGE_MAX), merged in split order
     float ms[MERGE_MAX], ls[MERGE_MAX], os[MERGE_MAX][8];

@@ -219,6 +219,12 @@ __device__ __forceinline__ f32x4_t load16_dev(__amdgpu_buffer_rsrc_t r, int off)
 __device__ __forceinline__ void store16_dev(__amdgpu_buffer_rsrc_t r, int off, f32x4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16);
 }
+__device__ __forceinline__ float load4_dev(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 16));
+}
+__device__ __forceinline__ void store4_dev(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 16);
+}
 
 static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
 
