@@ -7,7 +7,9 @@ The default run measures both halves in one invocation on random-init Qwen3-4B b
 (seed 0), greedy decoding through the engine's own ``generate()``:
 
 * ``value`` (B = 1, configs[1] "c2": a 128-token uniform-random prompt, 256 decode steps);
-* ``b32`` (B = 32, configs[3] "c4": 8192-token prompts, 256 decode steps, ~37 GiB of KV cache).
+* ``b32`` (B = 32, configs[3] "c4": 8192-token prompts, 256 decode steps, ~37 GiB of KV cache);
+* ``c3`` (B = 8, configs[2]) and ``c5`` (the speculative verify step, configs[4]) as further
+  blocks of the same line, so that every decode config is timed in the default run.
 
 Each is timed as follows. The batch state is built, certified and its step graph recorded
 first (untimed); the prompt forward gives ``ttft_s``; ``W`` warm-up steps run; then the
@@ -477,6 +479,23 @@ def main():
             "mfma": mfma_utilisation(eng, torch),
             "vs_b1": round(r4["value"] / res["value"], 3),
         }
+        # The other two decode configs, so that every one is timed in the default run.
+        B3, S3, N3 = CONFIGS["c3"]
+        K3 = args.steps if args.steps is not None else N3 - 1 - W
+        r3 = run_decode(eng, torch, cfg, B3, S3, N3, K3, W)
+        out["c3"] = {
+            "metric": "decode tok/s at B=8 (Qwen3-4B bf16)", "value": r3["value"], "unit": "tok/s",
+            "steps": r3["steps"], "ms_per_step": r3["ms_per_step"], "ttft_s": r3["ttft_s"],
+            "config": {"workload": f"c3: Qwen3-4B, B={B3}, prompts {S3}, {N3} greedy decode steps",
+                       "global_batch": B3, "seq_len": S3, "decode_steps": N3},
+            "step_roofline": r3["step_roofline"],
+        }
+        engine_mod.CONFIG["spec_k"] = SPEC_T - 1
+        B5, S5, N5 = CONFIGS["c5"]
+        r5 = bench_verify(eng, torch, cfg, B5, S5, args.steps if args.steps is not None else N5, W)
+        engine_mod.CONFIG["spec_k"] = 0
+        out["c5"] = {k: r5[k] for k in ("metric", "value", "unit", "steps", "ms_per_step", "positions_per_s",
+                                        "config", "roofline", "step_roofline")}
     if not args.no_cpu_baseline:
         try:
             out["cpu_baseline"] = cpu_baseline(eng, cfg, CONFIGS["c2"][1])
