@@ -597,28 +597,37 @@ __global__ void __launch_bounds__(256, 2) pf_attn_kernel(PfAttnParams p) {
 
 
 // Wide form of the prompt attention (qwen_attn_prefill for chunks of more than 16 tokens):
-// 8 wavefronts x 2 query tiles per workgroup, i.e. 64 query tokens x the 4 heads of the GQA group
-// = 256 query rows over the same 64-key K / V block in LDS. Wavefront w owns tokens 8 w .. 8 w + 7
+// 4 wavefronts x 2 query tiles per workgroup, i.e. 32 query tokens x the 4 heads of the GQA group
+// = 128 query rows over the same 64-key K / V block in LDS. Wavefront w owns tokens 8 w .. 8 w + 7
 // (tile mt: tokens 8 w + 4 mt .. + 3), so every K fragment read from LDS feeds both tiles' MFMAs
-// and each staged K / V byte serves four times as many query rows as in pf_attn_kernel.
-constexpr int AW2 = 8;               // wavefronts per workgroup
+// and each staged K / V byte serves twice as many query rows as in pf_attn_kernel. Two
+// workgroups share a CU (64 KB of LDS each), so the two wavefronts on a SIMD belong to different
+// workgroups with their own barriers and drift apart: one's softmax runs under the other's MFMAs
+// (measured on MI355X at the 32 x 512-token chunks: 2-3 % faster than one 8-wavefront
+// workgroup of 64 tokens per CU, 20 % on the first chunk).
+constexpr int AW2 = 4;               // wavefronts per workgroup
 constexpr int AQ2 = AW2 * 2 * 4;     // query tokens per workgroup (2 tiles of 4 tokens per wavefront)
+constexpr int AGPW = AKB / 4 / AW2;  // 4-row groups of a K / V block staged by each wavefront
 
 // The score tiles are computed transposed, S^T = K Q^T (K as the MFMA's A operand, Q^T as B).
 // Lane (q, r) then holds query r's scores for keys 16 nt + 4 q + i, which is already the
-// B-operand layout of O^T += V^T P^T once the k-slots of the PV product are ordered (32 kk + 4 q + j, 32 kk + 16 + 4 q + j): P goes from the score
-// accumulators into the PV MFMA through packed bf16 conversions, with no LDS round trip, and the
-// V^T fragments are transposed LDS reads in that same key order. Softmax state is one (m, l)
-// per lane and tile; a query's 64 scores sit on 4 lanes (r, r + 16, r + 32, r + 48), so a block
-// maximum is 15 in-lane maxima and 2 cross-lane steps. The causal mask is applied only to blocks
-// that reach past the wavefront's first token. exp(x - m) is evaluated as exp2((x - m) log2 e)
-// with scale folded in; rounding points as pf_attn_kernel (P rounded to bf16 for PV, l from the
-// unrounded P, O normalised in fp32, then rounded). exp2 is the hardware v_exp_f32: a P below
-// 2^-126 of the block maximum flushes to 0, far under bf16's resolution of the row sum.
+// B-operand layout of O^T += V^T P^T once the k-slots of the PV product are ordered
+// (32 kk + 4 q + j, 32 kk + 16 + 4 q + j): P goes from the score accumulators into the PV MFMA
+// through packed bf16 conversions, with no LDS round trip, and the V^T fragments are transposed
+// LDS reads in that same key order. Softmax state is one (m, l) per lane and tile; a query's 64
+// scores sit on 4 lanes (r, r + 16, r + 32, r + 48), so a block maximum is 15 in-lane maxima and
+// 2 cross-lane steps. The causal mask is applied only to blocks that reach past the wavefront's
+// first token. exp(x - m) is evaluated as exp2((x - m) log2 e) with scale folded in, and the
+// rescale factor as exp2((m_old - m_new) scale log2 e), exactly 1 when the maximum is unchanged:
+// a block that is fully masked for a query leaves that query's state bit for bit as it was, so
+// the result does not depend on how many such blocks a workgroup walks. Rounding points as
+// pf_attn_kernel (P rounded to bf16 for PV, l from the unrounded P, O normalised in fp32, then
+// rounded). exp2 is the hardware v_exp_f32: a P below 2^-126 of the block maximum flushes to 0,
+// far under bf16's resolution of the row sum.
 __device__ __forceinline__ float xlane_max4(float v) { return xor32_max(xor16_max(v)); }
 __device__ __forceinline__ float xlane_sum4(float v) { return xor32_sum(xor16_sum(v)); }
 
-__global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams p) {
+__global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams p) {
   // K / V blocks in 256-byte rows with no padding (direct-to-LDS loads fill 1 KB runs), swizzled
   // so that the fragment reads stay conflict-free: K's 16-byte chunk c of key row r at c ^ (r % 16)
   // (the S^T operand reads 16 rows of one chunk), V's 32-byte block j of row r at j ^ (r % 8) (a
@@ -670,23 +679,24 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
   const int wave_first = p.p0 + t_lo + 8 * wave;  // every query of the wavefront sees keys <= this
   const float c = p.scale * 1.4426950408889634f;  // scale * log2(e)
 
-  // K / V staging by direct global -> LDS loads: wavefront w fills key rows 8 w .. 8 w + 7 of a
-  // block (two 1 KB runs of 4 rows each for K and for V); lane l lands at row 4 (2 w + i) + l / 16,
+  // K / V staging by direct global -> LDS loads: wavefront w fills key rows 16 w .. 16 w + 15 of
+  // a block (four 1 KB runs of 4 rows each for K and for V); lane l lands at row
+  // 4 (AGPW w + i) + l / 16,
   // physical chunk l % 16, so it loads the logical chunk the swizzle puts there. Keys past kmax
   // read slot 0, a finite row every query's P weighs with exactly 0, so a stale or non-finite
   // slot never enters.
   const int srow = lane >> 4, spc = lane & 15;
   const unsigned lds_k = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.k[0][0][0];
   const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
-  // (K and V are issued separately, so a block's four loads per wavefront do not go out in one
+  // (K and V are issued separately, so a block's eight loads per wavefront do not go out in one
   // burst)
   auto issue_kv = [&](int blk, int buf, bool k) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = 4 * (2 * wave + i) + srow;   // row of the block
+    for (int i = 0; i < AGPW; ++i) {
+      const int r = 4 * (AGPW * wave + i) + srow;   // row of the block
       const int key = blk * AKB + r;
       const long long row = (long long)(key < kmax ? key : 0) * AD;
-      const unsigned off = (unsigned)((buf * AKB + 4 * (2 * wave + i)) * 256);
+      const unsigned off = (unsigned)((buf * AKB + 4 * (AGPW * wave + i)) * 256);
       if (k) lds_dma16(kbase + row + (spc ^ (r & 15)) * 8, lds_k + off);            // logical K chunk
       else lds_dma16(vbase + row + (2 * ((spc >> 1) ^ (r & 7)) + (spc & 1)) * 8, lds_v + off);  // V chunk
     }
@@ -744,7 +754,7 @@ __global__ void __launch_bounds__(AW2 * 64, 1) pf_attn_wide_kernel(PfAttnParams 
       mx = xlane_max4(mx);
       const float mn = fmaxf(m[mt], mx);
       const float mc = mn * c;
-      const float alpha = __builtin_amdgcn_exp2f(m[mt] * c - mc);
+      const float alpha = __builtin_amdgcn_exp2f((m[mt] - mn) * c);  // 1 exactly if mn == m
       float pr[4][4];
       float psum = 0.f;
 #pragma unroll
