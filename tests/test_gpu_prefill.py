@@ -122,6 +122,25 @@ def test_attn_prefill_first_query_sees_only_slot_zero(qops):
         assert torch.equal(out[:, 0, h], vc[:, h // 4, 0])
 
 
+@pytest.mark.parametrize("p0,T,split", [(17, 300, 150), (0, 256, 100), (3, 97, 40)])
+def test_attn_prefill_independent_of_chunking(qops, p0, T, split):
+    """A query's output does not depend on the chunk it is computed in: one chunk of T tokens
+    equals the same positions computed as two chunks (both longer than 16 tokens, so both take
+    the wide kernel), bit for bit. The workgroup holding a position walks a different number
+    of key blocks in the two layouts, and the extra blocks are fully masked for it, so this
+    holds only if a fully masked block leaves the online-softmax state exactly as it was."""
+    g = torch.Generator().manual_seed(p0 + T)
+    B, Nkv, D, CAP = 2, 8, 128, 1024
+    kc = _bf16(B, Nkv, CAP, D, gen=g).to(DEV)
+    vc = _bf16(B, Nkv, CAP, D, gen=g).to(DEV)
+    q = _bf16(B, T, 4 * Nkv, D, gen=g, scale=2.0).to(DEV)
+    scale = D ** -0.5
+    whole = qops.attn_prefill(q, kc, vc, p0, scale).cpu()
+    first = qops.attn_prefill(q[:, :split].contiguous(), kc, vc, p0, scale).cpu()
+    second = qops.attn_prefill(q[:, split:].contiguous(), kc, vc, p0 + split, scale).cpu()
+    assert torch.equal(whole, torch.cat([first, second], dim=1))
+
+
 # ---------------------------------------------------------------- engine prompt forward
 
 @pytest.fixture(scope="module")
