@@ -225,6 +225,14 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, unsigned lds_addr) {
                : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// The same load with a wavefront-uniform base in SGPRs and a 32-bit per-lane byte offset (the
+// instruction's saddr form): no 64-bit address arithmetic per load.
+__device__ __forceinline__ void lds_dma16_so(const void* sbase, unsigned voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_addr)
+               : "memory", "m0");
+}
 
 constexpr int PWM = 256;   // rows per workgroup
 constexpr int PWN = 256;   // weight rows (output columns before SwiGLU) per workgroup
@@ -690,15 +698,31 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
   const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
   // (K and V are issued separately, so a block's eight loads per wavefront do not go out in one
   // burst)
-  auto issue_kv = [&](int blk, int buf, bool k) __attribute__((always_inline)) {
+  // A lane's byte offset within a block is the same for every block: row r's logical chunk,
+  // r * 256 + chunk * 16. Whole blocks (all keys below kmax) add the block to the scalar base;
+  // the workgroup's last block, if it reaches past kmax, takes the clamped per-lane form.
+  unsigned koff[AGPW], voff[AGPW];
 #pragma unroll
-    for (int i = 0; i < AGPW; ++i) {
-      const int r = 4 * (AGPW * wave + i) + srow;   // row of the block
-      const int key = blk * AKB + r;
-      const long long row = (long long)(key < kmax ? key : 0) * AD;
-      const unsigned off = (unsigned)((buf * AKB + 4 * (AGPW * wave + i)) * 256);
-      if (k) lds_dma16(kbase + row + (spc ^ (r & 15)) * 8, lds_k + off);            // logical K chunk
-      else lds_dma16(vbase + row + (2 * ((spc >> 1) ^ (r & 7)) + (spc & 1)) * 8, lds_v + off);  // V chunk
+  for (int i = 0; i < AGPW; ++i) {
+    const int r = 4 * (AGPW * wave + i) + srow;
+    koff[i] = (unsigned)(r * 256 + (spc ^ (r & 15)) * 16);                          // logical K chunk
+    voff[i] = (unsigned)(r * 256 + (2 * ((spc >> 1) ^ (r & 7)) + (spc & 1)) * 16);  // V chunk
+  }
+  auto issue_kv = [&](int blk, int buf, bool k) __attribute__((always_inline)) {
+    const bf16_t* base = k ? kbase : vbase;
+    const unsigned lds0 = (k ? lds_k : lds_v) + (unsigned)((buf * AKB + 4 * AGPW * wave) * 256);
+    if ((blk + 1) * AKB <= kmax) {
+      const bf16_t* sb = base + (long long)blk * AKB * AD;
+#pragma unroll
+      for (int i = 0; i < AGPW; ++i) lds_dma16_so(sb, k ? koff[i] : voff[i], lds0 + i * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < AGPW; ++i) {
+        const int r = 4 * (AGPW * wave + i) + srow;   // row of the block
+        const int key = blk * AKB + r;
+        const unsigned cb = (k ? koff[i] : voff[i]) - (unsigned)(r * 256);  // chunk within the row
+        lds_dma16_so(base, key < kmax ? (unsigned)key * 256u + cb : cb, lds0 + i * 1024);
+      }
     }
   };
 
@@ -744,6 +768,7 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
     }
     // online softmax per tile (one query per lane); P^T as packed bf16 B fragments
     uint4 pb[2][2];
+    float alpha[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       float mx = st[mt][0][0];
@@ -754,7 +779,7 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
       mx = xlane_max4(mx);
       const float mn = fmaxf(m[mt], mx);
       const float mc = mn * c;
-      const float alpha = __builtin_amdgcn_exp2f((m[mt] - mn) * c);  // 1 exactly if mn == m
+      alpha[mt] = __builtin_amdgcn_exp2f((m[mt] - mn) * c);  // 1 exactly if mn == m
       float pr[4][4];
       float psum = 0.f;
 #pragma unroll
@@ -764,16 +789,21 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
           pr[nt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], c, -mc));  // masked: 0
           psum += pr[nt][i];
         }
-      l[mt] = l[mt] * alpha + psum;
+      l[mt] = l[mt] * alpha[mt] + psum;
       m[mt] = mn;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
         pb[mt][kk] = make_uint4(f2bf2(pr[2 * kk][0], pr[2 * kk][1]), f2bf2(pr[2 * kk][2], pr[2 * kk][3]),
                                 f2bf2(pr[2 * kk + 1][0], pr[2 * kk + 1][1]), f2bf2(pr[2 * kk + 1][2], pr[2 * kk + 1][3]));
+    }
+    // rescale O only when some query's maximum moved (alpha is exactly 1 otherwise)
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
 #pragma unroll
-      for (int nd = 0; nd < 8; ++nd)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[mt][nd][i] *= alpha;
+        for (int nd = 0; nd < 8; ++nd)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[mt][nd][i] *= alpha[mt];
     }
     // O^T += V^T P^T: A = V^T rows (dims) 16 nd + r, k-slots j -> key 32 kk + 4 q + j (lo) and
     // 32 kk + 16 + 4 q + j (hi), by transpose reads of 4 keys x 16 dims (source lane s ->
