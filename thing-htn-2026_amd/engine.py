@@ -47,7 +47,7 @@ BF16 = torch.bfloat16
 CONFIG = {
     "graphs": True,          # replay one HIP graph per decode step
     "inflight": 4,           # decode steps queued on the device ahead of the consumer
-    "prefill_tokens": 32768, # rows (sequences x positions) per prompt-forward chunk
+    "prefill_tokens": 65536, # rows (sequences x positions) per prompt-forward chunk
     "cap_round": 256,        # KV capacity granularity (a later call with a smaller need reuses the state)
     "group_rows": 32,        # sequences per decode row group (the kernels take at most 32 rows)
     # Exact speculative decoding (engine/engine.py:79-82): prompt-lookup drafts of spec_k tokens
