@@ -34,6 +34,11 @@
 //   and shared by the 4 wavefronts: S = Q K^T and O += P V on the matrix cores, online
 //   softmax in the accumulator layout, V^T fragments by ds_read_b64_tr_b16 (as in
 //   attention_mfma.hip). Workgroups with the most keys are launched first.
+//
+// The large shapes take the wide forms, each described at its definition below:
+// pf_gemm_wide_kernel (N a multiple of 256: persistent 256 x 256 tiles, both operands by
+// direct global -> LDS loads) and pf_attn_wide_kernel (chunks of more than 16 tokens: 32
+// query tokens per 4-wavefront workgroup, two workgroups per CU).
 #include "common.h"
 
 namespace {
