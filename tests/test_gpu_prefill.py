@@ -6,7 +6,8 @@ Bars: GEMMs at the reference's op-certification tolerance (atol 1e-2, rtol 1/64,
 ``engine/engine.py:425-429``) plus a two-hot case whose expected bits are closed-form (exact);
 attention atol 2e-2 (``tests/test_torch_ref.py:264``); the engine's per-layer hidden states within
 2e-2 relative and its first token under the greedy rule (the oracle's argmax unless its top-2 gap
-is below 1e-2).
+is below 1e-2). Chunking is exact: the attention, and the whole prompt forward, give the same bits
+however the positions are cut into chunks (more than 16 tokens each).
 """
 
 import pytest
@@ -181,3 +182,34 @@ def test_engine_prefill_matches_oracle(qwen4b_two_layers, monkeypatch, B, S, chu
     top2 = lg.topk(2, dim=-1).values
     ok = (lg.argmax(-1) == first.cpu()) | ((top2[:, 0] - top2[:, 1]) < 1e-2)
     assert bool(ok.all()), (first, lg.argmax(-1))
+
+
+def test_engine_prefill_bitexact_across_chunk_sizes(qwen4b_two_layers, monkeypatch):
+    """The prompt forward does not depend on how the positions are cut into chunks. A GEMM
+    row accumulates over k in a fixed order wherever it sits in the launch; the norms and RoPE
+    work row by row; and the chunk attention gives the same bits for a query however many
+    fully masked key blocks its workgroup walks. So three chunks of 128, 128 and 44 tokens
+    (256 rows each for B = 2; every chunk longer than 16 tokens, so all take the wide attention
+    kernel) and one chunk of 300 tokens must write the same K / V, leave the same hidden
+    states for the last positions and emit the same first tokens, bit for bit."""
+    import engine as engine_mod
+    eng, _, cfg = qwen4b_two_layers
+    B, S = 2, 300
+    g = torch.Generator().manual_seed(7)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
+    runs = {}
+    for rows in (256, 65536):
+        monkeypatch.setitem(engine_mod.CONFIG, "prefill_tokens", rows)
+        first, hidden = eng.prefill_hidden(prompt)
+        caches = [(eng.state.kcache(l)[:, :, :S].cpu().clone(), eng.state.vcache(l)[:, :, :S].cpu().clone())
+                  for l in range(cfg["num_hidden_layers"])]
+        runs[rows] = (first.cpu(), [h.cpu().view(B, -1, h.shape[-1]) for h in hidden], caches)
+    (f_small, h_small, c_small), (f_one, h_one, c_one) = runs[256], runs[65536]
+    assert h_small[0].shape[1] == 44 and h_one[0].shape[1] == S   # last chunk: positions 256 .. 299
+    for l, ((k0, v0), (k1, v1)) in enumerate(zip(c_small, c_one)):
+        assert torch.equal(k0, k1), f"layer {l} K cache differs"
+        assert torch.equal(v0, v1), f"layer {l} V cache differs"
+    tail = h_small[0].shape[1]
+    for l, (a, b) in enumerate(zip(h_small, h_one)):
+        assert torch.equal(a, b[:, S - tail:]), f"layer {l} hidden states differ"
+    assert torch.equal(f_small, f_one)
