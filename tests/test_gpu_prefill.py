@@ -123,6 +123,34 @@ def test_attn_prefill_first_query_sees_only_slot_zero(qops):
         assert torch.equal(out[:, 0, h], vc[:, h // 4, 0])
 
 
+def test_attn_prefill_keys_past_2_pow_24(qops):
+    """A cache of more than 2^24 slots, where a key's byte offset in its (sequence, head) slab
+    (256 bytes a row) passes 2^32. All keys are zero, so every visible score is 0 and each
+    query averages the value rows it sees; one value row is nonzero and lies in the
+    workgroup's last, partial key block. Query t (position p0 + t) sees it when p0 + t >= j*,
+    and then returns that row times 1 / (p0 + t + 1) (the row sum in fp32); earlier queries
+    return 0 exactly."""
+    B, Nkv, D = 1, 1, 128
+    CAP = (1 << 24) + 128
+    p0, T = (1 << 24) + 10, 40
+    jstar = (1 << 24) + 20
+    kc = torch.zeros(B, Nkv, CAP, D, dtype=BF16, device=DEV)
+    vc = torch.zeros_like(kc)
+    row = (torch.arange(D, dtype=torch.float32) / 8 + 1).to(BF16)
+    vc[0, 0, jstar] = row.to(DEV)
+    q = _bf16(B, T, 4 * Nkv, D, gen=torch.Generator().manual_seed(5)).to(DEV)
+    got = qops.attn_prefill(q, kc, vc, p0, D ** -0.5).cpu().view(B, T, 4 * Nkv, D).float()
+    del kc, vc
+    for t in range(T):
+        if p0 + t < jstar:
+            assert not bool(got[0, t].any()), f"query {t} sees no nonzero value row"
+            continue
+        inv = 1.0 / torch.tensor(float(p0 + t + 1), dtype=torch.float32)
+        want = (row.float() * inv).to(BF16).float()
+        for h in range(4 * Nkv):
+            assert torch.allclose(got[0, t, h], want, rtol=2 ** -7, atol=0), f"query {t} head {h}"
+
+
 @pytest.mark.parametrize("p0,T,split", [(17, 300, 150), (0, 256, 100), (3, 97, 40)])
 def test_attn_prefill_independent_of_chunking(qops, p0, T, split):
     """A query's output does not depend on the chunk it is computed in: one chunk of T tokens

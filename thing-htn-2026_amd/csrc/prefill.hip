@@ -696,16 +696,19 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
   // a block (four 1 KB runs of 4 rows each for K and for V); lane l lands at row
   // 4 (AGPW w + i) + l / 16,
   // physical chunk l % 16, so it loads the logical chunk the swizzle puts there. Keys past kmax
-  // read slot 0, a finite row every query's P weighs with exactly 0, so a stale or non-finite
-  // slot never enters.
+  // read slot kmax - 1, a row of this chunk's keys (written before the attention runs, so
+  // finite) that every query's P weighs with exactly 0 there: a stale or non-finite slot never
+  // enters.
   const int srow = lane >> 4, spc = lane & 15;
   const unsigned lds_k = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.k[0][0][0];
   const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
   // (K and V are issued separately, so a block's eight loads per wavefront do not go out in one
   // burst)
   // A lane's byte offset within a block is the same for every block: row r's logical chunk,
-  // r * 256 + chunk * 16. Whole blocks (all keys below kmax) add the block to the scalar base;
-  // the workgroup's last block, if it reaches past kmax, takes the clamped per-lane form.
+  // r * 256 + chunk * 16, added to the block's address in the scalar base. In the
+  // workgroup's last block, if it reaches past kmax, rows at or past kmax read row kmax - 1
+  // instead (still within the block, so every offset stays below 16 KB whatever the cache
+  // capacity).
   unsigned koff[AGPW], voff[AGPW];
 #pragma unroll
   for (int i = 0; i < AGPW; ++i) {
@@ -714,19 +717,18 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
     voff[i] = (unsigned)(r * 256 + (2 * ((spc >> 1) ^ (r & 7)) + (spc & 1)) * 16);  // V chunk
   }
   auto issue_kv = [&](int blk, int buf, bool k) __attribute__((always_inline)) {
-    const bf16_t* base = k ? kbase : vbase;
+    const bf16_t* sb = (k ? kbase : vbase) + (long long)blk * AKB * AD;
     const unsigned lds0 = (k ? lds_k : lds_v) + (unsigned)((buf * AKB + 4 * AGPW * wave) * 256);
     if ((blk + 1) * AKB <= kmax) {
-      const bf16_t* sb = base + (long long)blk * AKB * AD;
 #pragma unroll
       for (int i = 0; i < AGPW; ++i) lds_dma16_so(sb, k ? koff[i] : voff[i], lds0 + i * 1024);
     } else {
+      const int last = kmax - 1 - blk * AKB;   // last row of the block below kmax (>= 0)
 #pragma unroll
       for (int i = 0; i < AGPW; ++i) {
         const int r = 4 * (AGPW * wave + i) + srow;   // row of the block
-        const int key = blk * AKB + r;
-        const unsigned cb = (k ? koff[i] : voff[i]) - (unsigned)(r * 256);  // chunk within the row
-        lds_dma16_so(base, key < kmax ? (unsigned)key * 256u + cb : cb, lds0 + i * 1024);
+        const unsigned off = k ? koff[i] : voff[i];
+        lds_dma16_so(sb, r <= last ? off : off - (unsigned)((r - last) * 256), lds0 + i * 1024);
       }
     }
   };
