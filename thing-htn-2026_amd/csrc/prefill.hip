@@ -692,13 +692,12 @@ __global__ void __launch_bounds__(AW2 * 64, 2) pf_attn_wide_kernel(PfAttnParams 
   const int wave_first = p.p0 + t_lo + 8 * wave;  // every query of the wavefront sees keys <= this
   const float c = p.scale * 1.4426950408889634f;  // scale * log2(e)
 
-  // K / V staging by direct global -> LDS loads: wavefront w fills key rows 16 w .. 16 w + 15 of
-  // a block (four 1 KB runs of 4 rows each for K and for V); lane l lands at row
-  // 4 (AGPW w + i) + l / 16,
-  // physical chunk l % 16, so it loads the logical chunk the swizzle puts there. Keys past kmax
-  // read slot kmax - 1, a row of this chunk's keys (written before the attention runs, so
-  // finite) that every query's P weighs with exactly 0 there: a stale or non-finite slot never
-  // enters.
+  // K / V staging by direct global -> LDS loads: wavefront w fills key rows 16 w .. 16 w + 15
+  // of a block (four 1 KB runs of 4 rows each for K and for V). Lane l lands at row
+  // 4 (AGPW w + i) + l / 16, physical chunk l % 16, so it loads the logical chunk the swizzle
+  // puts there. Keys past kmax read slot kmax - 1, one of this chunk's keys (written before the
+  // attention runs, so finite), and every query weighs them with P = 0 exactly: a stale or
+  // non-finite slot never enters.
   const int srow = lane >> 4, spc = lane & 15;
   const unsigned lds_k = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.k[0][0][0];
   const unsigned lds_v = (unsigned)(uintptr_t)(__attribute__((address_space(3))) pv4*)&sm.kv.v[0][0][0];
