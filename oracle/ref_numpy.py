@@ -25,9 +25,10 @@ def rb(x) -> np.ndarray:
 
 
 def rms_norm(x, w, eps):
-    """``torch_ref.py:47-58``: bf16(x * rsqrt(mean(x^2) + eps)), then * gain, rounded."""
+    """``torch_ref.py:47-58``: bf16(x * rsqrt(mean(x^2) + eps)), then * gain, rounded; the mean is
+    the fp32 sum times fp32(1/N) (``engine/kernels/rmsnorm.py:87-88``)."""
     x = np.asarray(x, F32)
-    var = (np.sum(x * x, axis=-1, keepdims=True, dtype=F32) / F32(x.shape[-1])).astype(F32)
+    var = (np.sum(x * x, axis=-1, keepdims=True, dtype=F32) * F32(1.0 / x.shape[-1])).astype(F32)
     r = (F32(1.0) / np.sqrt(var + F32(eps))).astype(F32)
     return rb(np.asarray(w, F32) * rb(x * r))
 

@@ -60,6 +60,41 @@ def test_add_rms_norm(qops, rows, n):
     assert_bf16_close_ulp(y.cpu(), y_ref, 1, 2e-3, "add_rms_norm")
 
 
+def test_rms_norm_mean_form_every_kernel(qops):
+    """The RMSNorm mean is ``sum(x^2) * fp32(1/N)`` in every kernel that normalises the hidden
+    width (``engine/kernels/rmsnorm.py:87-88``): on rows whose sums of squares are exact in any
+    order (``helpers.MEAN_FORM_CASES``) the result is bit-exact, and the case elements take the
+    product form's value, which a division by N would round differently. One-hot weight rows
+    make a fused projection's output equal its normalised input element."""
+    from helpers import mean_form_rows
+    x, cols, y_mul, _ = mean_form_rows(seed=3)
+    Mr, K = x.shape
+    rows = torch.arange(Mr)
+    w1 = torch.ones(K, dtype=BF16)
+    want_n = R.rms_norm(x, w1, EPS)
+    assert torch.equal(want_n[rows, cols].float(), y_mul)
+    xd, w1d = x.to(DEV), w1.to(DEV)
+    assert torch.equal(qops.rms_norm(xd, w1d, EPS).cpu(), want_n)
+    h, y = qops.add_rms_norm(xd, torch.zeros_like(xd), w1d, EPS)
+    assert torch.equal(h.cpu(), x) and torch.equal(y.cpu(), want_n)
+    N = 6144    # the QKV projection's width: the skinny, stream-K and rectangle launches all take it
+    g = torch.Generator().manual_seed(8)
+    sel = torch.randint(0, K, (N,), generator=g)
+    sel[:Mr] = cols
+    w = torch.zeros(N, K, dtype=BF16)
+    w[torch.arange(N), sel] = 1.0
+    want = R.linear(want_n, w)
+    assert torch.equal(want[rows, rows].float(), y_mul)
+    t = qops.tile_weight(w.to(DEV))
+    for cfg in (None, (1, 8, 0), qops.rect_config(Mr, N, K)):
+        got = qops.fused_linear(xd, t, cfg, norm_w=w1d, eps=EPS).cpu()
+        assert torch.equal(got, want), f"fused_linear cfg={cfg}"
+    wd = w.to(DEV)
+    for r0 in range(0, Mr, 2):
+        got = qops.gemv(xd[r0:r0 + 2].contiguous(), wd, norm_w=w1d, eps=EPS).cpu()
+        assert torch.equal(got, want[r0:r0 + 2]), f"gemv rows {r0}..{r0 + 1}"
+
+
 def test_rms_norm_zero_row(qops):
     x = torch.zeros(2, 2560, dtype=BF16)
     w = torch.ones(2560, dtype=BF16)

@@ -62,6 +62,21 @@ def test_rms_norm_bit_exact(rows, n):
     assert torch.equal(got, want)
 
 
+def test_rms_norm_mean_form_differs_from_cpu_module():
+    """On the CPU, ``Qwen3RMSNorm``'s ``mean`` divides the sum by N; the reference's kernels and
+    torch's GPU ``mean`` multiply it by fp32(1/N) (``engine/kernels/rmsnorm.py:87-88``), which the
+    oracle follows. On the discriminating rows of ``helpers.MEAN_FORM_CASES`` the CPU module gives
+    the division's value and the oracle the product's; elsewhere they agree bit for bit."""
+    from helpers import mean_form_rows
+    x, cols, y_mul, y_div = mean_form_rows()
+    mod = Qwen3RMSNorm(x.shape[1], eps=EPS).to(BF16)
+    rows = torch.arange(len(cols))
+    with torch.no_grad():
+        want = mod(x)
+    got = R.rms_norm(x, mod.weight.data, EPS)
+    assert torch.equal(want[rows, cols].float(), y_div) and torch.equal(got[rows, cols].float(), y_mul)
+
+
 def test_rms_norm_flat_rows_match_3d():
     gen = torch.Generator().manual_seed(1234)
     mod = _norm_module(2560, gen)

@@ -3,8 +3,9 @@ entry point it mirrors (``qwen_attn_decode_mfma``), through the C ABI.
 
 Both run the same kernels on the same inputs, so the bar is bit-exact: the attention output and
 the K/V slots the call writes. Two calls in a row on the shared scratch (the second with a
-smaller input, so stale partials and counters of the first would show), and a shape that needs
-more than the fixed scratch is refused with status 1004 before anything is launched.
+smaller input, so stale partials and counters of the first would show); the first call of the
+process recorded into a HIP graph and replayed; a shape that needs more than the fixed scratch is
+refused with status 1004 before anything is launched.
 """
 
 import pytest
@@ -37,6 +38,42 @@ def _case(B, T, CAP, Nkv, seed):
 def _tables(P, D=128):
     from oracle import ref_torch as R
     return R.rope_tables(P, 5e6, D)
+
+
+def test_noalloc_first_call_recorded_in_a_graph(qops):
+    """The process's first call of the entry point on the device (its scratch-address lookup
+    included) is recorded into a HIP graph (``torch.cuda.CUDAGraph``); every replay, with eager
+    work and synchronisations between them, gives the workspace entry point's output and cache
+    writes bit for bit. Defined first in this module so it is that first call."""
+    cos, sin = _tables(4096)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    scale = 128 ** -0.5
+    B, T, CAP, Nkv, S = 8, 1, 2304, 8, 4
+    qkv, kc, vc, pos, qn, kn = _case(B, T, CAP, Nkv, 71)
+    args = (qkv.to(DEV), qn.to(DEV), kn.to(DEV), 1e-6, cos, sin, pos.to(DEV), T)
+    kc_g, vc_g = kc.to(DEV), vc.to(DEV)
+    out = torch.empty(B, T, 4 * Nkv * 128, dtype=BF16, device=DEV)
+    torch.cuda.synchronize()
+    # recorded under inference mode, as the engine records its step graphs (the process's graph
+    # generator state is created by the first recording, in whichever mode that ran)
+    with torch.inference_mode():
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            qops.attn_decode_mfma_noalloc(*args, kc_g, vc_g, scale, S, out=out, waves=8)
+        kc1, vc1 = kc.to(DEV), vc.to(DEV)
+        ws = qops.attn_mfma_workspace(B, T, Nkv, S, DEV)
+        want = qops.attn_decode_mfma(*args, kc1, vc1, scale, S, workspace=ws, waves=8)
+        for r in range(3):
+            out.zero_()
+            kc_g.copy_(kc)
+            vc_g.copy_(vc)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, want), f"replay {r}: outputs differ"
+            assert torch.equal(kc_g, kc1) and torch.equal(vc_g, vc1), f"replay {r}: cache writes differ"
+            qops.attn_decode_mfma(*args, kc1, vc1, scale, S, workspace=ws, waves=8)   # eager work between replays
+            torch.cuda.synchronize()
+        del graph
 
 
 @pytest.mark.parametrize("order", ["big_then_small"])

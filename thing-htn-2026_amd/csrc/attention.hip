@@ -78,7 +78,7 @@ __device__ __forceinline__ void norm_rope_head(float* x, const bf16_t* gain, con
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   ss += __shfl_xor(ss, 4, 64);
-  const float rinv = 1.0f / sqrtf(ss / (float)ATT_D + eps);
+  const float rinv = rms_rinv(ss, ATT_D, eps);
   float g[16], cs[16], sn[16];
   unpack8(*reinterpret_cast<const uint4*>(gain + 8 * c), g);
   unpack8(*reinterpret_cast<const uint4*>(gain + 64 + 8 * c), g + 8);

@@ -83,7 +83,7 @@ __device__ __forceinline__ void mload2_dev(const float* q, float& a, float& b) {
 __device__ __forceinline__ void mnorm_rope(float& x0, float& x1, float g0, float g1, float c0, float c1, float s0,
                                            float s1, float eps) {
   const float ss = wave_sum_dpp(add_rn(mul_rn(x0, x0), mul_rn(x1, x1)));
-  const float rinv = 1.0f / sqrtf(ss / (float)MD + eps);
+  const float rinv = rms_rinv(ss, MD, eps);
   const float y0 = rbf(mul_rn(g0, rbf(mul_rn(x0, rinv))));
   const float y1 = rbf(mul_rn(g1, rbf(mul_rn(x1, rinv))));
   x0 = rbf(add_rn(rbf(mul_rn(y0, c0)), rbf(mul_rn(-y1, s0))));
@@ -684,6 +684,21 @@ __global__ void __launch_bounds__(256) zero_words_kernel(unsigned* p, int n) {
   if (i < n) p[i] = 0u;
 }
 
+// Argument checks shared by qwen_attn_decode_mfma_ex and the allocation-free variant (everything
+// but the workspace), so that a refused call has launched nothing.
+int mfma_args_status(const void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                     const void* sin_tab, const int32_t* positions, const void* k_cache, const void* v_cache,
+                     const void* out, int B, int T, int Nq, int Nkv, int D, int CAP, int P, int num_splits, int waves,
+                     int flags) {
+  if (flags & ~QWEN_ATTN_KV_CACHED) return QWEN_EARG;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !k_cache || !v_cache || !out)
+    return QWEN_ENULL;
+  if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || CAP <= 0 || P <= 0) return QWEN_EARG;
+  if (num_splits < 1 || num_splits > MERGE_MAX || (waves != 4 && waves != 8)) return QWEN_EARG;
+  if ((long long)B * Nkv > 0x7fffffffLL) return QWEN_EARG;
+  return QWEN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -700,12 +715,9 @@ int qwen_attn_decode_mfma_ex(const void* qkv, const void* q_norm_w, const void* 
                              void* workspace, long long workspace_bytes, int B, int T, int Nq, int Nkv, int D,
                              int CAP, int P, float eps, float scale, int num_splits, int waves, int flags,
                              hipStream_t stream) {
-  if (flags & ~QWEN_ATTN_KV_CACHED) return QWEN_EARG;
-  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !k_cache || !v_cache || !out)
-    return QWEN_ENULL;
-  if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || CAP <= 0 || P <= 0) return QWEN_EARG;
-  if (num_splits < 1 || num_splits > MERGE_MAX || (waves != 4 && waves != 8)) return QWEN_EARG;
-  if ((long long)B * Nkv > 0x7fffffffLL) return QWEN_EARG;
+  const int st = mfma_args_status(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out, B, T,
+                                  Nq, Nkv, D, CAP, P, num_splits, waves, flags);
+  if (st != QWEN_OK) return st;
   if (B == 0) return QWEN_OK;
   const long long need = qwen_attn_mfma_workspace_bytes(B, T, Nkv, num_splits);
   if (need > 0 && (!workspace || workspace_bytes < need)) return workspace ? QWEN_EWORKSPACE : QWEN_ENULL;
@@ -732,8 +744,9 @@ int qwen_attn_decode_mfma_noalloc(const void* qkv, const void* q_norm_w, const v
                                   const void* cos_tab, const void* sin_tab, const int32_t* positions, void* k_cache,
                                   void* v_cache, void* out, int B, int T, int Nq, int Nkv, int D, int CAP, int P,
                                   float eps, float scale, int num_splits, int waves, int flags, hipStream_t stream) {
-  if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || num_splits < 1 || num_splits > MERGE_MAX)
-    return QWEN_EARG;
+  const int st = mfma_args_status(qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out, B, T,
+                                  Nq, Nkv, D, CAP, P, num_splits, waves, flags);
+  if (st != QWEN_OK) return st;
   const long long need = qwen_attn_mfma_workspace_bytes(B, T, Nkv, num_splits);
   if (need > NOALLOC_SCRATCH_BYTES) return QWEN_ESCRATCH;
   if (need == 0 || B == 0)

@@ -69,6 +69,15 @@ __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
+// RMSNorm factor rsqrt(mean + eps) of a row of n values whose squares sum to sumsq. The mean
+// is the fp32 sum times the fp32 reciprocal of n, as the reference's kernels compute it
+// (engine/kernels/rmsnorm.py:87-88 passes inv_n = 1 / n_cols; gemm_fused.py:168 1 / K), not a
+// division by n (up to 1 fp32 ulp apart for n = 2560); product and sum rounded one at a time.
+__device__ __forceinline__ float rms_rinv(float sumsq, int n, float eps) {
+  const float inv_n = __fdiv_rn(1.0f, (float)n);
+  return 1.0f / sqrtf(add_rn(mul_rn(sumsq, inv_n), eps));
+}
+
 // Unpack 8 bf16 held in a uint4 (little-endian pairs) to fp32.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};

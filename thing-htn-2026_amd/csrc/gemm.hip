@@ -147,7 +147,7 @@ struct AOperand {
           }
         }
         s = xor32_sum(xor16_sum(s));  // the row's four quarters (lanes r, r + 16, r + 32, r + 48)
-        rinv[mt] = 1.0f / sqrtf(s / (float)p.K + p.eps);
+        rinv[mt] = rms_rinv(s, p.K, p.eps);
       }
     }
   }
@@ -686,7 +686,7 @@ __global__ void __launch_bounds__(64 * WPG) rect_gemm_kernel(GemmParams p, int G
       float sacc = 0.f;
 #pragma unroll
       for (int u = 0; u < RECT_PPL; ++u) sacc += pv[i][u] * (lane + 64 * u < nu ? 1.f : 0.f);  // keeps every load used
-      rinv = 1.0f / sqrtf(wave_sum_dpp(sacc) / (float)p.K + p.eps);
+      rinv = rms_rinv(wave_sum_dpp(sacc), p.K, p.eps);
     }
     if (m < p.M) {
 #pragma unroll

@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(GemvParams p) {
     for (int m = 0; m < M; ++m) {
       float t = 0.f;
       for (int w = 0; w < WAVES; ++w) t += red[w * M + m];
-      rinv[m] = 1.0f / sqrtf(t / (float)K + p.eps);
+      rinv[m] = rms_rinv(t, K, p.eps);
     }
 #pragma unroll
     for (int q = 0; q < XC; ++q) {

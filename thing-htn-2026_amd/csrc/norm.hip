@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(NORM_THREADS) rms_norm_kernel(
     }
   }
   const float total = block_sum(ss, red);
-  const float rinv = 1.0f / sqrtf(total / (float)N + eps);
+  const float rinv = rms_rinv(total, N, eps);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int ci = threadIdx.x + c * NORM_THREADS;

@@ -55,7 +55,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_cache_kernel(
   ss += dpp_mov_f<0xB1>(ss);
   ss += dpp_mov_f<0x4E>(ss);
   ss += dpp_mov_f<0x141>(ss);
-  const float rinv = 1.0f / sqrtf(ss / (float)D + eps);
+  const float rinv = rms_rinv(ss, D, eps);
 
   const bf16_t* gain = head < Nq ? qw : kw;
   float gl[8], gh[8], cl[8], ch[8], sl[8], sh[8];

@@ -9,7 +9,7 @@ HIP kernels only.
 
 Rounding points (``bf16(.)`` is round-to-nearest-even):
 
-* RMSNorm: ``y = w * bf16(x * rsqrt(mean(x^2) + eps))``, the product rounded once.
+* RMSNorm: ``y = w * bf16(x * rsqrt(sum(x^2) * (1/N) + eps))``, the product rounded once.
 * residual: ``h = bf16(x + r)``.
 * projections: fp32 accumulation, one rounding; the fused epilogues round the product first
   (``bf16(res + bf16(acc))``, ``bf16(bf16(silu(bf16(g))) * bf16(u))``).
@@ -27,9 +27,11 @@ F32 = torch.float32
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """Qwen3 RMSNorm over the last dim (``engine/kernels/torch_ref.py:47-58``)."""
+    """Qwen3 RMSNorm over the last dim (``engine/kernels/torch_ref.py:47-58``); the mean is the
+    fp32 sum times fp32(1/N) (``engine/kernels/rmsnorm.py:87-88``)."""
     xf = x.to(F32)
-    n = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)).to(BF16)
+    var = xf.square().sum(-1, keepdim=True) * torch.tensor(1.0 / x.shape[-1], dtype=F32, device=x.device)
+    n = (xf * torch.rsqrt(var + eps)).to(BF16)
     return (n.to(F32) * w.to(F32)).to(BF16)
 
 
