@@ -50,6 +50,11 @@ class CpuQwen3:
         self.cos_tab = self.sin_tab = None
         # the LM head: tied to the embedding unless the weights hold their own (engine/engine.py:225-226)
         self.lm_head = weights.get("lm_head", weights["embed"])
+        # decode-step attention ``f(q, k_cache, v_cache, lengths, scale)`` and prompt attention
+        # ``f(q, k, v, scale)``: the twin's global-maximum form by default; ``R.attn_decode_flash`` /
+        # ``R.causal_prefill_attention_flash`` restate the running maximum of flash attention
+        self.attention = R.attn_decode
+        self.prefill_attention = R.causal_prefill_attention
 
     # ------------------------------------------------------------- weights
     @classmethod
@@ -115,7 +120,7 @@ class CpuQwen3:
         qkv = R.linear(n, w["w_qkv"])
         q = R.qk_norm_rope_cache(qkv, w["q_norm"], w["k_norm"], self.eps, self.cos_tab, self.sin_tab,
                                  pos, T, self.k_cache[l][:B], self.v_cache[l][:B])
-        a = R.attn_decode(q, self.k_cache[l][:B], self.v_cache[l][:B], pos + T, self.scale)
+        a = self.attention(q, self.k_cache[l][:B], self.v_cache[l][:B], pos + T, self.scale)
         o = R.linear(a.view(M, -1), w["w_o"])
         h, n = R.add_rms_norm(h, o, w["ln2"], self.eps)
         p = R.silu_mul(R.linear(n, w["w_gu"]))
@@ -179,7 +184,7 @@ class CpuQwen3:
             kc, vc = self.k_cache[l][:B], self.v_cache[l][:B]
             q = R.qk_norm_rope_cache(qkv, w["q_norm"], w["k_norm"], self.eps, self.cos_tab, self.sin_tab,
                                      pos, S, kc, vc)
-            a = R.causal_prefill_attention(q, kc[:, :, :S], vc[:, :, :S], self.scale)
+            a = self.prefill_attention(q, kc[:, :, :S], vc[:, :, :S], self.scale)
             o = R.linear(a, w["w_o"])
             h, n = R.add_rms_norm(h, o, w["ln2"], self.eps)
             d = R.linear(R.silu_mul(R.linear(n, w["w_gu"])), w["w_down"])

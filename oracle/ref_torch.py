@@ -30,12 +30,15 @@ F32 = torch.float32
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """Qwen3 RMSNorm over the last dim. Restates ``engine/kernels/torch_ref.py:47-58``.
 
-    fp32 sum of squares, mean, ``rsqrt(var + eps)``; the normalised value is
-    rounded to bf16 first and only then multiplied by the bf16 gain (that
-    product rounded once).
+    fp32 sum of squares times the fp32 reciprocal ``1/N`` (the reference's
+    mean: ``engine/kernels/rmsnorm.py:87-88`` passes ``inv_n = 1 / n_cols``,
+    and torch's GPU ``mean`` multiplies by that factor; torch's CPU ``mean``
+    divides by ``N`` instead, up to 1 fp32 ulp away), ``rsqrt(var + eps)``;
+    the normalised value is rounded to bf16 first and only then multiplied by
+    the bf16 gain (that product rounded once).
     """
     xf = x.to(F32)
-    var = xf.pow(2).mean(-1, keepdim=True)
+    var = xf.pow(2).sum(-1, keepdim=True) * torch.tensor(1.0 / x.shape[-1], dtype=F32)
     n = (xf * torch.rsqrt(var + eps)).to(x.dtype)
     return w * n
 
@@ -166,6 +169,102 @@ def attn_decode(q, k_cache, v_cache, lengths, scale):
     o = torch.matmul(e.to(BF16).to(F32), vf) / l
     o = o.reshape(B, Nkv, G, T, D).permute(0, 3, 1, 2, 4)
     return o.to(BF16).reshape(B, T, Nq * D).contiguous()
+
+
+FLASH_BLOCK_N = 64        # keys per block of the reference's Triton kernel (attention.py:80)
+FLASH_NEG = -1e30         # its finite stand-in for -inf (attention.py:84-87)
+
+
+def choose_num_splits(B: int, Nkv: int) -> int:
+    """The reference's split count (``engine/kernels/attention.py:94-110``): the smallest power of
+    two ``S`` with ``B * Nkv * S >= 264``, at most 32."""
+    bh, s = max(1, B * Nkv), 1
+    while bh * s < 264 and s < 32:
+        s *= 2
+    return s
+
+
+def reference_schedule(num_splits: int, block_n: int = FLASH_BLOCK_N):
+    """The key blocks of the reference's Triton decode attention (``attention.py:139-214``) as a
+    schedule ``f(length, T) -> lanes``: split ``s`` covers ``[s * chunk, min((s + 1) * chunk, length))``
+    with ``chunk = cdiv(length, S)`` rounded up to whole blocks, walked in blocks of ``block_n``."""
+    def lanes(length: int, T: int):
+        chunk = -(-length // num_splits)
+        chunk = -(-chunk // block_n) * block_n
+        out = []
+        for s in range(num_splits):
+            start, end = s * chunk, min(s * chunk + chunk, length)
+            out.append([(n0, min(n0 + block_n, end)) for n0 in range(start, end, block_n)])
+        return out
+    return lanes
+
+
+def attn_decode_flash(q, k_cache, v_cache, lengths, scale, schedule=None):
+    """Decode attention with the reference kernel's online softmax. Restates
+    ``engine/kernels/attention.py:115-275`` (``_attn_partial_kernel`` + ``_attn_reduce_kernel``).
+
+    Same visibility, scale and rounding points as ``attn_decode``, but the un-normalised
+    probabilities of a block are ``exp(s - m)`` against the running maximum ``m`` of its lane
+    (the keys seen so far), rounded to bf16 for the PV product; earlier blocks are rescaled by
+    ``exp(m_old - m_new)`` in fp32 (``attention.py:199-214``); the lanes' ``(m, l, acc)`` merge by
+    log-sum-exp and one division, rounded to bf16 once (``attention.py:253-275``). ``attn_decode``
+    instead rounds every probability against the row's global maximum, so the two differ in the
+    last bf16 bit of many P values.
+
+    ``schedule(length, T) -> lanes``: per lane, the key ranges ``[k0, k1)`` it walks in order
+    (default: ``reference_schedule(choose_num_splits(B, Nkv))``, the reference kernel's), or a list
+    of such, one per sequence. A key beyond a query's limit ``length - (T - 1 - t)`` is masked.
+    Returns ``[B, T, Nq * D]`` bf16."""
+    B, T, Nq, D = q.shape
+    Nkv = k_cache.shape[1]
+    G = Nq // Nkv
+    if schedule is None:
+        schedule = reference_schedule(choose_num_splits(B, Nkv))
+    schedules = schedule if isinstance(schedule, (list, tuple)) else [schedule] * B
+    out = torch.empty((B, T, Nkv, G, D), dtype=BF16)
+    neg = torch.tensor(FLASH_NEG, dtype=F32)
+    for b in range(B):
+        schedule = schedules[b]
+        L = int(lengths[b])
+        qf = q[b].to(F32).reshape(T, Nkv, G, D).permute(1, 0, 2, 3).reshape(Nkv, T * G, D)   # row t*G + g
+        limit = L - (T - 1 - torch.arange(T * G) // G)                                       # [T*G]
+        parts = []
+        for lane in schedule(L, T):
+            m = torch.full((Nkv, T * G), FLASH_NEG, dtype=F32)
+            l = torch.zeros((Nkv, T * G), dtype=F32)
+            acc = torch.zeros((Nkv, T * G, D), dtype=F32)
+            for k0, k1 in lane:
+                n = torch.arange(k0, k1)
+                kf = k_cache[b, :, k0:k1].to(F32)
+                vf = v_cache[b, :, k0:k1].to(F32)
+                vis = (n[None, :] < limit[:, None])[None]                                    # [1, R, n]
+                s = torch.where(vis, torch.matmul(qf, kf.transpose(-1, -2)) * scale, neg)
+                m_new = torch.maximum(m, s.amax(-1))
+                alpha = torch.exp(m - m_new)
+                p = torch.where(vis, torch.exp(s - m_new[..., None]), torch.zeros((), dtype=F32))
+                l = l * alpha + p.sum(-1)
+                acc = acc * alpha[..., None] + torch.matmul(p.to(BF16).to(F32), vf)
+                m = m_new
+            parts.append((m, l, acc))
+        ms = torch.stack([p[0] for p in parts])
+        mx = ms.amax(0)
+        w = torch.exp(ms - mx)
+        lt = (w * torch.stack([p[1] for p in parts])).sum(0)
+        at = (w[..., None] * torch.stack([p[2] for p in parts])).sum(0)
+        o = (at / lt[..., None]).reshape(Nkv, T, G, D).permute(1, 0, 2, 3)
+        out[b] = o.to(BF16)
+    return out.reshape(B, T, Nq * D).contiguous()
+
+
+def causal_prefill_attention_flash(q, k, v, scale, block_n: int = FLASH_BLOCK_N):
+    """``causal_prefill_attention`` with the online softmax of flash attention, as the reference's
+    prefill SDPA computes it on the GPU (``engine/engine.py:1123-1179``): every query walks the keys
+    in blocks of ``block_n`` from key 0, rounding P to bf16 against its running maximum
+    (``attn_decode_flash`` with one lane)."""
+    B, S = q.shape[0], q.shape[1]
+    lengths = torch.full((B,), S, dtype=torch.int32)
+    one_lane = reference_schedule(1, block_n)
+    return attn_decode_flash(q, k, v, lengths, scale, one_lane).reshape(B * S, -1)
 
 
 def causal_prefill_attention(q, k, v, scale):

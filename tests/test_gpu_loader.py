@@ -85,7 +85,7 @@ def test_checkpoint_loads_and_decodes(tmp_path, tied, rope_form, shards):
         prompt = _prompt(B, S, B * 31 + S)
         steps = list(eng.generate(prompt, N))
         tokens = [[steps[n][b] for n in range(N)] for b in range(B)]
-        assert_greedy_parity(ref, prompt, tokens, f"checkpoint tied={tied} {rope_form} B={B}")
+        assert_greedy_parity(ref, prompt, tokens, f"checkpoint tied={tied} {rope_form} B={B}", engine=eng)
     # per-layer hidden states of one decode step
     prompt = _prompt(2, 16, 7)
     list(eng.generate(prompt, 1))

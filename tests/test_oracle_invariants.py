@@ -75,6 +75,25 @@ def test_generator_statistics_and_determinism():
 
 # ------------------------------------------------------------- norms / silu / rope
 
+def test_rms_norm_mean_is_sum_times_reciprocal():
+    """The mean is ``sum(x^2) * fp32(1/N)`` (``engine/kernels/rmsnorm.py:87-88``), not ``sum / N``:
+    on rows whose sum of squares is exact in any order, the two forms round the case element to
+    different bf16 values (``helpers.MEAN_FORM_CASES``), and both restatements give the product's."""
+    from helpers import mean_form_rows
+    x, cols, y_mul, y_div = mean_form_rows()
+    w = torch.ones(x.shape[1], dtype=BF16)
+    rows = torch.arange(len(cols))
+    assert not torch.equal(y_mul, y_div)
+    assert torch.equal(R.rms_norm(x, w, EPS)[rows, cols].float(), y_mul)
+    assert np.array_equal(N.rms_norm(_np(x), _np(w), EPS)[rows.numpy(), cols.numpy()], y_mul.numpy())
+    h, y = R.add_rms_norm(x, torch.zeros_like(x), w, EPS)
+    assert torch.equal(h, x) and torch.equal(y[rows, cols].float(), y_mul)
+    # the same rows under a division by N (torch's CPU mean) give the other value
+    xf = x.float()
+    div = (xf * torch.rsqrt(xf.pow(2).sum(-1, keepdim=True) / x.shape[1] + EPS)).to(BF16)
+    assert torch.equal(div[rows, cols].float(), y_div)
+
+
 def test_rms_norm_closed_forms():
     w = (1.0 + torch.arange(256) / 256).to(BF16)
     assert torch.equal(R.rms_norm(torch.zeros(3, 256, dtype=BF16), w, EPS), torch.zeros(3, 256, dtype=BF16))
@@ -165,6 +184,106 @@ def test_attention_poisoned_slots_ignored():
     kc[0, :, 7:], vc[0, :, 7:] = float("nan"), float("inf")
     kc[1, :, 12:], vc[1, :, 12:] = float("nan"), float("inf")
     assert torch.equal(R.attn_decode(q, kc, vc, lens, 128 ** -0.5), clean)
+
+
+# Known answers of the running-maximum rounding (flash) against the global-maximum rounding (twin):
+# 64 keys of score 0 then one key of score a (scale 1); V = e0 for the 64 keys, e1 for the last.
+# Output dim 0 is 64 p0 / (64 e + 1), e = exp(-a): p0 = e in fp32 for the flash form (the block's
+# P = 1 exactly, rescaled by alpha = e), p0 = bf16(e) for the twin. Closed forms in float64, rounded
+# to bf16 (each at least 1.9e-4 from a rounding boundary), found by a scan of bf16 a in [0.5, 4).
+FLASH_KAT = [(0.5, 0.9765625, 0.97265625), (0.55859375, 0.97265625, 0.96875), (0.5859375, 0.97265625, 0.96875)]
+
+
+@pytest.mark.parametrize("a,want_flash,want_twin", FLASH_KAT)
+def test_flash_attention_rounds_p_against_the_running_maximum(a, want_flash, want_twin):
+    D = 128
+    q = torch.zeros(1, 1, 4, D, dtype=BF16)
+    q[..., 0] = a
+    kc = torch.zeros(1, 1, 80, D, dtype=BF16)
+    kc[0, 0, 64, 0] = 1.0
+    vc = torch.zeros(1, 1, 80, D, dtype=BF16)
+    vc[0, 0, :64, 0] = 1.0
+    vc[0, 0, 64, 1] = 1.0
+    lens = torch.tensor([65], dtype=torch.int32)
+    flash = R.attn_decode_flash(q, kc, vc, lens, 1.0).view(4, D)
+    twin = R.attn_decode(q, kc, vc, lens, 1.0).view(4, D)
+    assert flash[:, 0].tolist() == [want_flash] * 4 and twin[:, 0].tolist() == [want_twin] * 4
+    # one split of two blocks gives the same closed form as two one-block splits (the reference's 32)
+    two_blocks = R.attn_decode_flash(q, kc, vc, lens, 1.0, R.reference_schedule(1)).view(4, D)
+    assert torch.equal(two_blocks, flash)
+
+
+def test_flash_schedule_and_split_rule_known_answers():
+    assert [R.choose_num_splits(B, 8) for B in (1, 4, 8, 32, 64)] == [32, 16, 8, 2, 1]
+    lanes = R.reference_schedule(4)(650, 1)     # chunk = cdiv(650, 4) = 163 -> 192 (whole 64-key blocks)
+    assert lanes == [[(0, 64), (64, 128), (128, 192)], [(192, 256), (256, 320), (320, 384)],
+                     [(384, 448), (448, 512), (512, 576)], [(576, 640), (640, 650)]]
+    assert R.reference_schedule(8)(100, 1)[2:] == [[]] * 6     # splits past the length are empty
+
+
+@pytest.mark.parametrize("B,T,lengths,CAP", [(2, 1, [5, 200], 256), (2, 3, [70, 12], 128), (1, 5, [650], 700)])
+def test_flash_attention_float64_and_twin(B, T, lengths, CAP):
+    q, kc, vc, lens = _attn_case(B, T, lengths, CAP, 21)
+    scale = 128 ** -0.5
+    got = R.attn_decode_flash(q, kc, vc, lens, scale)
+    want = N.attn_decode(_np(q), _np(kc), _np(vc), lens.numpy(), scale)
+    assert np.abs(got.float().numpy() - want).max() <= 1e-2
+    # the twin and the flash form differ only through P's rounding point: within the reference's
+    # attention bar (atol 2e-2, tests/test_torch_ref.py:264), and equal up to fp32 summation
+    # order when one block spans every key (running maximum = global maximum)
+    twin = R.attn_decode(q, kc, vc, lens, scale)
+    assert (got.float() - twin.float()).abs().max() <= 2e-2
+    one = R.attn_decode_flash(q, kc, vc, lens, scale, lambda L, T: [[(0, L)]])
+    d = (one.float() - twin.float()).abs()
+    assert float(d.max()) <= 2 ** -7 * float(twin.float().abs().max()) and float((d > 0).float().mean()) <= 2e-3
+
+
+def test_flash_attention_single_key_and_poison():
+    q, kc, vc, _ = _attn_case(2, 1, [1, 1], 16, 12)
+    lens = torch.tensor([1, 1], dtype=torch.int32)
+    out = R.attn_decode_flash(q, kc, vc, lens, 128 ** -0.5)
+    assert torch.equal(out, vc[:, :, 0, :][:, :, None, :].expand(2, 2, 4, 128).reshape(2, 1, 8 * 128))
+    q, kc, vc, lens = _attn_case(2, 3, [7, 12], 16, 13)
+    clean = R.attn_decode_flash(q, kc, vc, lens, 128 ** -0.5)
+    kc[0, :, 7:], vc[0, :, 7:] = float("nan"), float("inf")
+    kc[1, :, 12:], vc[1, :, 12:] = float("nan"), float("inf")
+    assert torch.equal(R.attn_decode_flash(q, kc, vc, lens, 128 ** -0.5), clean)
+
+
+def test_flash_prefill_attention():
+    """The flash prompt attention (64-key blocks from key 0, one running maximum per query) within
+    the attention bar of the twin's, equal to it up to fp32 order while one block holds every key,
+    and equal, up to fp32 summation order, to the flash decode attention of each position on its
+    own (a causal prefix)."""
+    g = torch.Generator().manual_seed(31)
+    B, S, NQ, NKV, D = 2, 150, 8, 2, 128
+    q, k, v = _bf16(B, S, NQ, D, gen=g), _bf16(B, NKV, S, D, gen=g), _bf16(B, NKV, S, D, gen=g)
+    scale = D ** -0.5
+    flash = R.causal_prefill_attention_flash(q, k, v, scale)
+    twin = R.causal_prefill_attention(q, k, v, scale)
+    assert (flash.float() - twin.float()).abs().max() <= 2e-2
+    one = R.causal_prefill_attention_flash(q[:, :60], k[:, :, :60], v[:, :, :60], scale)
+    d = (one.float() - R.causal_prefill_attention(q[:, :60], k[:, :, :60], v[:, :, :60], scale).float()).abs()
+    assert float((d > 0).float().mean()) <= 2e-3
+    for p in (0, 63, 64, 149):
+        dec = R.attn_decode_flash(q[:, p:p + 1], k, v, torch.full((B,), p + 1, dtype=torch.int32), scale,
+                                  R.reference_schedule(1))
+        u = _ulps(_np(flash.view(B, S, -1)[:, p]), _np(dec[:, 0]))
+        assert u.max() <= 1 and (u > 0).mean() <= 1e-2, p
+
+
+def test_engine_schedule_covers_every_key_once():
+    from helpers import engine_schedule
+    for splits, waves, T, L in [(1, 8, 1, 129), (4, 8, 1, 2305), (8, 8, 5, 4101), (1, 4, 1, 40), (3, 8, 2, 7)]:
+        lanes = engine_schedule(splits, waves, T)(L, T)
+        assert len(lanes) == splits * waves
+        keys = sorted(k for lane in lanes for k0, k1 in lane for k in range(k0, k1))
+        assert keys == list(range(L)), (splits, waves, T, L)
+        last = lanes[-1]
+        new = (L - T, L)
+        first = (4 * T + 15) // 16 == 1 and waves != 4
+        assert last.index(new) == (0 if first else len(last) - 1)
+        assert all(k1 - k0 <= 32 for lane in lanes for k0, k1 in lane if (k0, k1) != new)
 
 
 # ------------------------------------------------------------- GEMM / argmax

@@ -650,13 +650,18 @@ class Engine:
         return verdict
 
     # ================================================================== prompt forward
-    def _prefill(self, ids: torch.Tensor, hidden=None) -> torch.Tensor:
+    def _prefill(self, ids: torch.Tensor, hidden=None, probe=None) -> torch.Tensor:
         """Prompt forward (``engine/engine.py:1181-1221``): fills the KV cache for positions
         ``[0, S)`` of every sequence and returns the first greedy token per sequence (``[B]``
         int64). The prompt runs in position chunks ``[p0, p1)`` of all ``B`` sequences
         (``prefill_tokens`` rows each); a chunk's attention reads the keys of earlier chunks
-        from the cache. ``hidden`` (a list) receives the residual stream after each layer for
-        the positions of the last chunk, ``[B * (p1 - p0), H]`` (row ``b * (p1 - p0) + t``)."""
+        from the cache. A chunk of more than 16 positions takes the wide attention kernel and
+        gives the same bits however the prompt is cut; a shorter last chunk takes the narrow
+        kernel, whose exponent and summation order differ (same bar, not the same bits).
+        ``hidden`` (a list) receives the residual stream after each layer for the positions of
+        the last chunk, ``[B * (p1 - p0), H]`` (row ``b * (p1 - p0) + t``); ``probe(l, p0, p1,
+        a, h)`` is called after every layer of every chunk with the attention output ``a [B,
+        p1 - p0, Nq * D]`` and the residual stream ``h`` (tests)."""
         st, s, dev = self.state, self.spec, self.device
         B, S = ids.shape
         chunk = max(1, min(S, CONFIG["prefill_tokens"] // B))
@@ -680,6 +685,8 @@ class Engine:
                 ops.gemm(p, w.down, residual=h, out=h)
                 if hidden is not None and last:
                     hidden.append(h.clone())
+                if probe is not None:
+                    probe(l, p0, p1, a, h)
         h_last = h.view(B, -1, s.H)[:, -1].contiguous()
         first = torch.empty((B,), dtype=torch.int64, device=dev)
         for r0 in range(0, B, 32):
@@ -785,13 +792,14 @@ class Engine:
         torch.cuda.synchronize()
         return trace
 
-    def prefill_hidden(self, input_ids, N: int = 1):
+    def prefill_hidden(self, input_ids, N: int = 1, probe=None):
         """Prompt forward of ``input_ids`` on a fresh batch state; returns ``(first [B], hidden)``
-        with the residual stream after each layer (positions of the last prompt chunk)."""
+        with the residual stream after each layer (positions of the last prompt chunk);
+        ``probe`` as in ``_prefill``."""
         ids = self._token_ids(input_ids)
         hidden = []
         with torch.inference_mode():
             self.prepare(ids.shape[0], ids.shape[1], N)
-            first = self._prefill(ids.to(self.device), hidden=hidden)
+            first = self._prefill(ids.to(self.device), hidden=hidden, probe=probe)
         torch.cuda.synchronize()
         return first, hidden
