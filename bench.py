@@ -12,10 +12,12 @@ The default run measures both halves in one invocation on random-init Qwen3-4B b
   blocks of the same line, so that every decode config is timed in the default run.
 
 Each is timed as follows. The batch state is built, certified and its step graph recorded
-first (untimed); the prompt forward gives ``ttft_s``; ``W`` warm-up steps run; then the
-decode steps launched between two device synchronisations are timed, so ``value`` = decoded
-tokens / wall seconds over exactly those steps. Weights and KV cache are resident in HBM; only
-token ids cross PCIe (8 bytes per sequence per step).
+first (untimed); the prompt forward gives ``ttft_s``; ``W`` warm-up steps run; then exactly
+``K`` decode steps of the same ``generate()`` are timed with HIP events on the launch stream
+(before the first timed launch, after the last), so ``value`` = B x K tokens / those seconds;
+the generation then runs to the config's length untimed. The c5 block of the default run
+replays at least its 200 verify steps. Weights and KV cache are resident in HBM; only token
+ids cross PCIe (8 bytes per sequence per step).
 
 ``roofline`` is for the dominant kernel of the workload, timed live with HIP events on the
 stream it runs on: at B = 1 the fused RMSNorm + gate/up GEMV + SwiGLU (44 % of a step's bytes),
@@ -254,35 +256,53 @@ def mfma_utilisation(eng, torch, reps=2):
 
 
 def run_decode(eng, torch, cfg, B, S, N, K, W):
-    """One greedy generate() of N tokens for B prompts of S tokens; K decode steps timed after W."""
+    """One greedy generate() of the config's N tokens (more if 1 + W + K asks for more) for B prompts
+    of S tokens; the W decode steps after the first token are untimed, the next K are timed with HIP
+    events recorded on the launch stream just before the (W + 1)-th step launch and just after the
+    (W + K)-th (exactly K steps of device time, the token pump's read-back included); the rest of
+    the generation runs untimed. ``decode_wall_tok_s``: all decode steps over host wall time."""
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g).tolist()
     total = max(N, 1 + W + K)
     with torch.inference_mode():
         eng.prepare(B, S, total)          # batch state, certification, step graph: untimed
     torch.cuda.synchronize()
-    gen = eng.generate(prompt, total)
-    t_pf = time.perf_counter()
-    next(gen)                              # prompt forward + first token
-    ttft = time.perf_counter() - t_pf
-    for _ in range(W):
-        next(gen)
-    torch.cuda.synchronize()
-    l0 = eng.counters["decode"]
-    t0 = time.perf_counter()
-    for _ in gen:
-        pass
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    steps = eng.counters["decode"] - l0
-    if steps <= 0:
-        sys.exit(f"bench.py: no decode step was launched inside the timed window (--steps {K})")
-    dt = t1 - t0
-    ms_step = dt / steps * 1e3
-    ctx_mid = S + 1 + W + steps / 2
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launched = [0]
+    plain = eng._plain
+
+    def timed_plain():
+        launched[0] += 1
+        if launched[0] == W + 1:
+            ev0.record(stream)
+        out = plain()
+        if launched[0] == W + K:
+            ev1.record(stream)
+        return out
+
+    eng._plain = timed_plain               # the token pump calls it once per decode step
+    try:
+        gen = eng.generate(prompt, total)
+        t_pf = time.perf_counter()
+        next(gen)                          # prompt forward + first token
+        ttft = time.perf_counter() - t_pf
+        t0 = time.perf_counter()
+        for _ in gen:
+            pass
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        del eng._plain
+    if launched[0] < W + K:
+        sys.exit(f"bench.py: only {launched[0]} decode steps were launched (warm-up {W} + timed {K})")
+    dt = ev0.elapsed_time(ev1) / 1e3
+    ms_step = dt / K * 1e3
+    ctx_mid = S + 1 + W + K / 2
     step_bytes = weight_bytes(cfg) + B * ctx_mid * kv_bytes_per_token(cfg)
     return {
-        "value": round(steps * B / dt, 2), "steps": steps, "ms_per_step": round(ms_step, 4), "ttft_s": round(ttft, 3),
+        "value": round(K * B / dt, 2), "steps": K, "ms_per_step": round(ms_step, 4), "ttft_s": round(ttft, 3),
+        "decode_wall_tok_s": round(launched[0] * B / wall, 2),
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "achieved_GBps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
                           "frac": round(step_bytes / (ms_step / 1e3) / HBM_PEAK, 4)},
@@ -460,8 +480,9 @@ def main():
         "roofline": roofline(avg, nbytes, name, first, what),
         "step_roofline": res["step_roofline"],
         "ttft_s": res["ttft_s"],
-        "steps_note": ("steps = decode steps launched inside the timed window; the engine queues up to "
-                       f"{engine_mod.CONFIG['inflight']} steps ahead, so those launched before it are not counted"),
+        "decode_wall_tok_s": res["decode_wall_tok_s"],
+        "steps_note": ("exactly `steps` decode steps of one generate() are timed (HIP events around their "
+                       "launches, after `warmup` untimed steps); the rest of the generation is untimed"),
     }
     if args.config == "default":
         B4, S4, N4 = CONFIGS["c4"]
@@ -492,7 +513,7 @@ def main():
         }
         engine_mod.CONFIG["spec_k"] = SPEC_T - 1
         B5, S5, N5 = CONFIGS["c5"]
-        r5 = bench_verify(eng, torch, cfg, B5, S5, args.steps if args.steps is not None else N5, W)
+        r5 = bench_verify(eng, torch, cfg, B5, S5, max(N5, args.steps or 0), W)   # at least its 200 steps
         engine_mod.CONFIG["spec_k"] = 0
         out["c5"] = {k: r5[k] for k in ("metric", "value", "unit", "steps", "ms_per_step", "positions_per_s",
                                         "config", "roofline", "step_roofline")}
