@@ -93,8 +93,8 @@ def parse():
     p.add_argument("--profile-sample", action="store_true",
                    help="run only the dominant kernel of --config (c2: gate/up GEMV, c4: attention) and a plain "
                         "1 GiB device copy, for rocprofv3 --pmc traffic runs; prints one JSON line")
-    p.add_argument("--profile-kernel", default="dominant", choices=["dominant", "o"],
-                   help="with --profile-sample: the dominant kernel, or the O projection")
+    p.add_argument("--profile-kernel", default="dominant", choices=["dominant", "o", "qkv"],
+                   help="with --profile-sample: the dominant kernel, or the O or QKV projection")
     return p.parse_args()
 
 
@@ -157,11 +157,42 @@ def time_gate_up(eng, torch, reps=3, T=1):
     return avg, nbytes, name
 
 
-def time_o_proj(eng, torch, reps=3):
-    """Average launch time of the O projection + residual (M = B rows, K = 4096), rotating over the 36
+def time_qkv(eng, torch, reps=3, T=1):
+    """Average launch time of the fused RMSNorm + QKV projection at M = B * T, rotating over the 36
     layers' weights. Returns (seconds, algorithmic bytes, kernel name)."""
     from qwen_hip import ops
-    b = eng.bufs(eng.state.groups[0], 1)
+    b = eng.bufs(eng.state.groups[0], T)
+    ops.sumsq16(b.h, out=b.psq)
+
+    def one(w):
+        if b.gemv:
+            ops.gemv(b.h, w.qkv_rows, norm_w=w.ln1, eps=eng.eps, out=b.qkv, cfg=b.gemv_cfg["qkv"],
+                     row_map=eng.w.qkv_map)
+        else:
+            ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=eng.eps, out=b.qkv, psq_in=b.psq,
+                             workspace=b.gemm_ws)
+
+    def sweep():
+        for w in eng.w.layers:
+            one(w)
+        return len(eng.w.layers)
+
+    sweep()
+    torch.cuda.synchronize()
+    avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
+    w0 = eng.w.layers[0].qkv
+    M = b.M
+    nbytes = w0.nbytes + M * w0.K * 2 + w0.K * 2 + M * w0.N * 2
+    name = ("gemv_kernel<%d, %d, true, 0>" % (M, b.gemv_cfg["qkv"][1]) if b.gemv
+            else ops.gemm_kernel_name(M, b.cfg["qkv"], True, ops.EPI_STORE))
+    return avg, nbytes, name
+
+
+def time_o_proj(eng, torch, reps=3, T=1):
+    """Average launch time of the O projection + residual (M = B * T rows, K = 4096), rotating over the
+    36 layers' weights. Returns (seconds, algorithmic bytes, kernel name)."""
+    from qwen_hip import ops
+    b = eng.bufs(eng.state.groups[0], T)
     a = b.a.view(b.M, -1)
     h2 = b.h.clone()
 
@@ -406,10 +437,13 @@ def cpu_baseline(eng, cfg, S, runs=3, target_s=6.0):
 
 
 def profile_sample(eng, torch, config, kernel="dominant"):
-    """Dominant-kernel (or ``kernel="o"``: O-projection) launches plus a copy of known size (the
-    FETCH_SIZE / WRITE_SIZE calibration)."""
+    """Dominant-kernel (or ``kernel="o"`` / ``"qkv"``: the O / QKV projection) launches at the config's
+    step width, plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
+    T = SPEC_T if config == "c5" else 1
     if kernel == "o":
-        avg, nbytes, name = time_o_proj(eng, torch, reps=1)
+        avg, nbytes, name = time_o_proj(eng, torch, reps=1, T=T)
+    elif kernel == "qkv":
+        avg, nbytes, name = time_qkv(eng, torch, reps=1, T=T)
     elif config == "c4":
         avg, nbytes, name = time_attention(eng, torch, reps=1)
     else:

@@ -21,11 +21,12 @@ maximum of 64-key blocks). The engine is held to the larger of the two, plus a s
 Hidden states: one decode step re-run at the last prompt position, with the engine's own K/V
 cache copied into the oracle (so the prompt forward's error does not enter), compared per layer:
 
-* local: the oracle's layer ``l`` applied to the engine's input of layer ``l``: within 2e-2
-  relative at every layer, with the engine's attention block schedule and
-  with the twin's;
-* accumulated: the oracle's whole step from the embedding against the engine's, next to the
-  reference kernel's own distance from the twin on the same step.
+* local: the oracle's layer ``l`` applied to the engine's input of layer ``l``: within 1e-2
+  relative at every layer with the twin's attention (half the north-star 2e-2) and within 5e-3
+  with the engine's attention block order;
+* accumulated: the oracle's whole step from the embedding against the engine's, within 1.25x the
+  reference kernel's own distance from the twin on the same step (+ 2e-3), and within that
+  distance (+ 2e-3) of the oracle run in the engine's block order.
 
 The oracle's weights are the engine's device weights copied to the host (the device generator is
 bit-identical to ``oracle/weights.py``: ``tests/test_gpu_ops.py``).
@@ -115,9 +116,15 @@ def rel(a, b):
     return float((a - b).norm() / b.norm())
 
 
-def check_hidden(name, eng, ref, prompt, local_bar=2e-2):
+def check_hidden(name, eng, ref, prompt):
     """Hidden states after each layer for one decode step (the last prompt token re-run at its
-    position) over the engine's K/V; returns the per-layer relative errors."""
+    position) over the engine's K/V; returns the per-layer relative errors. Bars, per layer:
+
+    * local error (the oracle's layer on the engine's input): <= 1e-2 with the twin's attention
+      (half the north-star 2e-2), <= 5e-3 with the engine's attention block order;
+    * accumulated error: within 1.25x (+ 2e-3) of the reference kernel's own distance from the
+      twin against the twin, and within that distance (+ 2e-3) against the oracle run in the
+      engine's block order."""
     B, Sp = len(prompt), len(prompt[0])
     list(eng.generate(prompt, 1))                                  # prompt forward + state
     tok = torch.tensor(prompt)[:, -1:]
@@ -160,9 +167,14 @@ def check_hidden(name, eng, ref, prompt, local_bar=2e-2):
     print(f"{name}: relative error per layer (splits {b.splits}, waves {b.attn_waves})")
     for k, v in rows.items():
         print(f"  {k:58s} " + " ".join(f"{r:.1e}" for r in v), flush=True)
-    for l in range(L):
-        for k in ("local, engine vs oracle (twin attention)", "local, engine vs oracle (engine's block schedule)"):
-            assert rows[k][l] <= local_bar, f"{name} layer {l}: {k} {rows[k][l]:.3e} > {local_bar}"
+    floor = rows["accumulated, reference kernel vs twin"]
+    bars = {"local, engine vs oracle (twin attention)": [1e-2] * L,
+            "local, engine vs oracle (engine's block schedule)": [5e-3] * L,
+            "accumulated, engine vs oracle (twin attention)": [1.25 * f + 2e-3 for f in floor],
+            "accumulated, engine vs oracle (engine's block schedule)": [f + 2e-3 for f in floor]}
+    for k, bar in bars.items():
+        for l in range(L):
+            assert rows[k][l] <= bar[l], f"{name} layer {l}: {k} {rows[k][l]:.3e} > {bar[l]:.3e}"
     return rows
 
 
