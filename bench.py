@@ -167,7 +167,7 @@ def time_qkv(eng, torch, reps=3, T=1):
     def one(w):
         if b.gemv:
             ops.gemv(b.h, w.qkv_rows, norm_w=w.ln1, eps=eng.eps, out=b.qkv, cfg=b.gemv_cfg["qkv"],
-                     row_map=eng.w.qkv_map, groups=8 if eng.w.qkv_map is not None else 1)
+                     row_map=eng.w.qkv_map)
         else:
             ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=eng.eps, out=b.qkv, psq_in=b.psq,
                              workspace=b.gemm_ws)

@@ -122,33 +122,6 @@ int qwen_attn_decode_mfma_noalloc(const void* qkv, const void* q_norm_w, const v
                                   void* out, int B, int T, int Nq, int Nkv, int D, int CAP, int P, float eps,
                                   float scale, int num_splits, int waves, int flags, hipStream_t stream);
 
-/* Workspace bytes of qwen_qkv_attn_decode for B sequences, Nkv KV heads and num_splits context
- * splits (0 if the shape is not supported): the attention's split workspace, then 4096 bytes of
- * hand-off words (256 projection and 64 attention generation flags, 256 projection XCC ids, then
- * the error word at byte offset 2304 of those 4096). Zeroed once by the caller and kept for every
- * launch of the shape: each launch raises every flag by one. */
-long long qwen_qkv_attn_workspace_bytes(int B, int Nkv, int num_splits);
-
-/* The decode step's RMSNorm + QKV projection and its attention (QK-norm + RoPE + K/V write +
- * GQA attention) in one launch, for B <= 2 sequences of one token: the same operators as
- * qwen_gemv_rowmap (epi 0, groups 8) followed by qwen_attn_decode_mfma_ex (T = 1, 8 wavefronts),
- * with bit-identical results. Replaces engine/engine.py:1104-1113 (add_rms_norm, _mm(w_qkv),
- * qk_norm_rope_cache, attn_decode). x [B, H] (the residual stream), w_qkv [N, H] row-major in
- * head-major order (block h of N / 8 rows is KV head group h: its query heads, key and value
- * rows), ln1 [H], row_map [N] int32 (row i's natural column), qkv [B, N] receives the projection
- * (natural layout); the attention arguments as qwen_attn_decode_mfma_ex. Needs Nkv = 8, Nq =
- * 4 Nkv, D = 128 and B * Nkv * num_splits <= 64: 256 workgroups, the attention workgroups of KV
- * head h on the XCD of the projection workgroups of its rows, which pass through that XCD's L2.
- * An attention workgroup waits inside the launch for its rows (a bounded wait: on expiry it
- * writes 1 to the workspace's error word and skips its output); one that finds a producer it
- * waited for on another XCD writes 2. The caller must check the word. No reference counterpart
- * (the reference launches these operators separately). */
-int qwen_qkv_attn_decode(const void* x, const void* w_qkv, const void* ln1, const int32_t* row_map, float eps,
-                         void* qkv, const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
-                         const void* sin_tab, const int32_t* positions, void* k_cache, void* v_cache, void* out,
-                         void* workspace, long long workspace_bytes, int B, int H, int Nq, int Nkv, int D, int CAP,
-                         int P, float scale, int num_splits, int flags, hipStream_t stream);
-
 /* Per-16-column partial sums of squares of a [M, K] bf16 matrix: psq[m, u] =
  * sum_{j<16} x[m, 16u + j]^2 in fp32. These are the RMSNorm statistics the normed
  * projections consume (psq_in below). No reference counterpart: it is the first
@@ -203,16 +176,13 @@ int qwen_gemv(const void* x, const void* w, void* out, int M, int N, int K, int 
               const void* residual, int epi, unsigned long long* amax, int grid, int waves, hipStream_t stream);
 
 /* qwen_gemv with the store epilogue (epi = 0) writing weight row i's output to column
- * row_map[i] (a permutation of [0, N), int32 on the device; row_map == NULL is qwen_gemv), and
- * the rows cut into `groups` equal contiguous groups (N and grid multiples of groups): workgroup
- * g is number g / groups of the grid / groups workgroups of group g % groups and owns an equal
- * share of that group's rows (groups = 1: rows [N*g/grid, N*(g+1)/grid)). No reference
- * counterpart: with a head-major QKV weight and groups = 8, every workgroup of XCD g mod 8
- * (workgroup g runs on XCD g mod 8) produces only rows of KV head group g mod 8, while the
- * output keeps its natural layout. */
+ * row_map[i] (a permutation of [0, N), int32 on the device; row_map == NULL is qwen_gemv).
+ * No reference counterpart: it lets a caller permute a weight's rows to choose which
+ * workgroup, and so which XCD, produces each output column while the output keeps its
+ * natural layout. */
 int qwen_gemv_rowmap(const void* x, const void* w, void* out, int M, int N, int K, int ld_out, const void* norm_w,
                      float eps, const void* residual, int epi, unsigned long long* amax, const int32_t* row_map,
-                     int groups, int grid, int waves, hipStream_t stream);
+                     int grid, int waves, hipStream_t stream);
 
 /* Packed argmax keys of an M-row LM head: QWEN_ARGMAX_SLOTS slots per row, slot s of row m at
  * amax[s * QWEN_ARGMAX_LD(M) + m] (uint64: monotone logit bits << 32 | ~index); the row's key

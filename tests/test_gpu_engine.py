@@ -208,26 +208,6 @@ def test_qwen4b_speculation_periodic(qwen4b_two_layers, monkeypatch):
     assert_greedy_parity(ref, prompt, tokens, "qwen4b-2L periodic speculation")
 
 
-def test_qwen4b_single_launch_qkv_attention(qwen4b_two_layers, monkeypatch):
-    """The opt-in single-launch QKV projection + attention (``CONFIG["fuse_qkv_attn"]``) on the
-    M <= 2 plain steps: the same tokens as the two-launch form (its kernels are the same bodies,
-    so bit-identical), greedy parity with the oracle, and no expired hand-off wait."""
-    import engine as engine_mod
-    eng, ref, cfg = qwen4b_two_layers
-    for B, S, N in [(1, 40, 6), (2, 300, 5)]:
-        prompt = _prompt(B, S, cfg["vocab_size"], 7 * B + S)
-        runs = {}
-        for fuse in (False, True):
-            monkeypatch.setitem(engine_mod.CONFIG, "fuse_qkv_attn", fuse)
-            eng.state = None                       # rebuild the batch state with this form
-            runs[fuse] = _run(eng, prompt, N, cfg["vocab_size"])
-            assert eng.state.bufs[(0, 1)].fused == fuse
-            eng.check_handoffs()
-        assert runs[True] == runs[False], f"B={B}: single launch changed the tokens"
-        assert_greedy_parity(ref, prompt, runs[True], f"qwen4b-2L single launch B={B}", engine=eng)
-    eng.state = None
-
-
 # --------------------------------------------------------------- warmup certification
 # engine/engine.py:407-486: every decode-step stage and every operator of the ops table is run
 # on the production shape against its twin; the engine refuses a shape that fails.

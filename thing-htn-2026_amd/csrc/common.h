@@ -235,33 +235,6 @@ __device__ __forceinline__ void store4_dev(__amdgpu_buffer_rsrc_t r, int off, fl
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 16);
 }
 
-// In-launch hand-off between the QKV projection's workgroups and the decode attention's
-// workgroups of one XCD (qwen_qkv_attn_decode). Generation flags, one per workgroup: a launch
-// raises every flag by one. Projection workgroup g stores its rows into the XCD's L2 (plain
-// stores), waits for them, then writes its generation to pflag[g]; an attention workgroup takes
-// its own generation from cflag, polls the flags of its group's projection workgroups with
-// L1-bypassing loads until all reach it, then writes it back. Projection workgroup g records
-// its XCC id in pxcc[g] when it starts, and the attention workgroup checks that every producer
-// it waited for ran on its own XCD (the hand-off goes through that XCD's L2); `err` receives 1
-// when a bounded wait expires and 2 when a producer ran on another XCD.
-struct QkvSync {
-  unsigned* pflag;  // [256] per projection workgroup
-  unsigned* cflag;  // [64] per attention workgroup
-  unsigned* pxcc;   // [256] per projection workgroup
-  unsigned* err;
-  int producers;    // projection workgroups per group
-  int spin_limit;   // polls before a wait gives up
-};
-
-// 32-bit load that bypasses the CU's L1 and reads the XCD's L2 (nt sc0): for values another
-// workgroup of the same XCD wrote during this launch.
-__device__ __forceinline__ unsigned load_l2(const void* p) {
-  return __builtin_amdgcn_raw_buffer_load_b32(coherent_rsrc(p), 0, 0, 3);
-}
-
-// The XCD (XCC id, 0 .. 7) this wavefront runs on.
-__device__ __forceinline__ int xcc_id() { return (int)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)); }
-
 static inline int qwen_status(hipError_t e) { return e == hipSuccess ? QWEN_OK : (int)e; }
 
 // Compute units of the current device (cached per device and translation unit; 0 on error).

@@ -66,10 +66,6 @@ CONFIG = {
     "xcd_heads": os.environ.get("QWEN_ENGINE_XCD_HEADS", "1") != "0",
     # Whole-KV-cache size up to which the decode attention reads K/V with cache-allocating loads.
     "kv_cached_max_bytes": int(os.environ.get("QWEN_ENGINE_KV_CACHED_MAX", str(128 << 20))),
-    # M <= 2 plain steps: the QKV projection and the attention in one launch (needs xcd_heads).
-    # Off by default: the in-launch hand-off (a flag poll is one L2 round trip, about 2 us while
-    # the projection streams its weights) costs more than the launch boundary it removes.
-    "fuse_qkv_attn": os.environ.get("QWEN_ENGINE_FUSE_QKV_ATTN", "0") == "1",
     "log": True,
 }
 
@@ -169,7 +165,7 @@ class StepBuffers:
     """Activation buffers, launch shapes and workspaces of one decode step over one row group
     (``rows`` sequences x ``T`` tokens); reused by every replay of that step."""
 
-    def __init__(self, spec: ModelSpec, rows: int, T: int, cap: int, device, fuse_qkv_attn: bool = False):
+    def __init__(self, spec: ModelSpec, rows: int, T: int, cap: int, device):
         M = rows * T
         self.rows, self.T, self.M = rows, T, M
         self.h = torch.zeros((M, spec.H), dtype=BF16, device=device)
@@ -206,11 +202,6 @@ class StepBuffers:
             "lm": ops.gemv_config(M, spec.V, spec.H, ops.GEPI_ARGMAX, device),
         } if self.gemv else None
         self.lm_cfg = ops.lm_head_config(M, spec.V, spec.H)
-        # M <= 2 plain steps: QKV projection + attention in one launch (head-major QKV weight)
-        self.fused = (fuse_qkv_attn and self.gemv and self.mfma_attn and T == 1 and self.attn_waves == 8
-                      and ops.qkv_attn_supported(rows, spec.Nkv, self.splits))
-        if self.fused:
-            self.attn_ws = ops.qkv_attn_workspace(rows, spec.Nkv, self.splits, device)
 
 
 class Engine:
@@ -247,26 +238,27 @@ class Engine:
 
     # ================================================================== weights
     def _qkv_xcd_order(self):
-        """Head-major row order of the M <= 2 QKV GEMV's weight: block h of the rows holds KV head
-        group h (its query heads, key and value rows, each in natural order), or None when the
+        """Row order of the M <= 2 QKV GEMV's weight in which the workgroups of one XCD produce
+        exactly one KV head group (its query heads, key and value rows), or None when the
         shapes do not allow it.
 
-        The GEMV runs with one row group per XCD (``groups = 8``): workgroup g, which runs on XCD
-        g mod 8, takes a share of block g mod 8, and the decode attention's workgroup for (sequence
-        b, KV head h), number b * Nkv + h, runs on XCD h. With Nkv = 8 head h's q / k / v rows are
-        then produced on the XCD whose L2 its attention workgroup reads, and the single-launch
-        QKV + attention form can hand them over inside the XCD. Outputs are stored at their natural
-        columns (the returned permutation as ``row_map``), so the qkv layout is unchanged.
+        Workgroup g of a launch runs on XCD g mod 8, the GEMV's workgroup g owns weight rows
+        [N g / G, N (g + 1) / G), and the decode attention's workgroup for (sequence b, KV
+        head h) is number b * Nkv + h. With Nkv = 8 and each head group exactly G / 8
+        workgroups of rows, the order below (outputs still stored at their natural columns)
+        leaves head h's q / k / v rows in the L2 of the XCD that runs its attention.
         Returns ``perm [N]``: reordered row p is natural row perm[p]."""
         s = self.spec
         N = s.qkv_width
         G, _ = ops.gemv_config(1, N, s.H, ops.GEPI_STORE, self.device)
         qd = (s.Nq // s.Nkv) * s.D
         grp = qd + 2 * s.D
-        if s.Nkv != XCDS or G % XCDS:
+        if s.Nkv != XCDS or N % G or G % XCDS or grp != (G // XCDS) * (N // G):
             return None
+        rows = N // G
         p = torch.arange(N, dtype=torch.int64)
-        h, i = p // grp, p % grp
+        g, j = p // rows, p % rows
+        h, i = g % XCDS, (g // XCDS) * rows + j
         k0, v0 = s.Nq * s.D, (s.Nq + s.Nkv) * s.D
         return torch.where(i < qd, h * qd + i,
                            torch.where(i < qd + s.D, k0 + h * s.D + (i - qd), v0 + h * s.D + (i - qd - s.D)))
@@ -455,19 +447,8 @@ class Engine:
         st = self.state
         key = (g.index, T)
         if key not in st.bufs:
-            fuse = CONFIG["fuse_qkv_attn"] and self.w.qkv_map is not None
-            st.bufs[key] = StepBuffers(self.spec, g.n, T, st.cap, self.device, fuse_qkv_attn=fuse)
+            st.bufs[key] = StepBuffers(self.spec, g.n, T, st.cap, self.device)
         return st.bufs[key]
-
-    def check_handoffs(self):
-        """Raise if a bounded in-launch wait of the single-launch QKV + attention form expired on
-        any step shape of the current batch (its output would be unwritten). Synchronises."""
-        st = self.state
-        if st is None:
-            return
-        for (gi, T), b in st.bufs.items():
-            if b.fused and ops.qkv_attn_failed(b.attn_ws):
-                raise RuntimeError(f"QKV + attention hand-off wait expired (row group {gi}, T={T})")
 
     # ================================================================== decode step
     def _layer(self, l: int, g: rt.RowGroup, b: StepBuffers, trace=None):
@@ -479,29 +460,22 @@ class Engine:
         kc, vc = g.kv[l]
         keep = (lambda t: trace.append(t.clone())) if trace is not None else (lambda t: None)
         M = b.M
-        # M <= 2: balanced row-major GEMVs (statistics computed in-kernel), the QKV projection and
-        # the attention in one launch where the shape allows; else MFMA GEMMs over the tiled
-        # weights, statistics from psq (left by whoever last wrote h).
-        if b.fused:
-            ops.qkv_attn_decode(b.h, w.qkv_rows, w.ln1, self.w.qkv_map, s.eps, b.qkv, w.q_norm, w.k_norm,
-                                self.cos_tab, self.sin_tab, g.pos, kc, vc, self.scale, b.splits, out=b.a,
-                                workspace=b.attn_ws, kv_cached=self.state.kv_cached)
-            keep(b.qkv)
+        # M <= 2: balanced row-major GEMVs (statistics computed in-kernel); else MFMA GEMMs over
+        # the tiled weights, statistics from psq (left by whoever last wrote h).
+        if b.gemv:
+            gc = b.gemv_cfg
+            ops.gemv(b.h, w.qkv_rows, norm_w=w.ln1, eps=s.eps, out=b.qkv, cfg=gc["qkv"], row_map=self.w.qkv_map)
         else:
-            if b.gemv:
-                ops.gemv(b.h, w.qkv_rows, norm_w=w.ln1, eps=s.eps, out=b.qkv, cfg=b.gemv_cfg["qkv"],
-                         row_map=self.w.qkv_map, groups=XCDS if self.w.qkv_map is not None else 1)
-            else:
-                ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=s.eps, out=b.qkv, psq_in=b.psq,
-                                 workspace=b.gemm_ws)
-            keep(b.qkv)
-            if b.mfma_attn:
-                ops.attn_decode_mfma(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc,
-                                     vc, self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves,
-                                     kv_cached=self.state.kv_cached)
-            else:
-                ops.attn_decode_fused(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc,
-                                      vc, self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves)
+            ops.fused_linear(b.h, w.qkv, b.cfg["qkv"], norm_w=w.ln1, eps=s.eps, out=b.qkv, psq_in=b.psq,
+                             workspace=b.gemm_ws)
+        keep(b.qkv)
+        if b.mfma_attn:
+            ops.attn_decode_mfma(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc, vc,
+                                 self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves,
+                                 kv_cached=self.state.kv_cached)
+        else:
+            ops.attn_decode_fused(b.qkv, w.q_norm, w.k_norm, s.eps, self.cos_tab, self.sin_tab, g.pos, b.T, kc, vc,
+                                  self.scale, b.splits, out=b.a, workspace=b.attn_ws, waves=b.attn_waves)
         keep(b.a)
         a = b.a.view(M, -1)
         if b.gemv:
@@ -667,7 +641,6 @@ class Engine:
                     check(name, tw.close(a_o, a_t, atol=1e-2, rtol=1e-2))
             g.pos.copy_(saved_pos)
         torch.cuda.synchronize()
-        self.check_handoffs()
         _log(f"certified rows={rows} T={T}: {verdict}")
         failed = [k for k, ok in verdict.items() if not ok]
         if failed:
@@ -772,7 +745,6 @@ class Engine:
         pump = rt.TokenPump(st.B, N, first, CONFIG["inflight"], k, self._plain, self._verify, policy,
                             self.counters)
         yield from pump
-        self.check_handoffs()
 
     # ================================================================== test / bench hooks
     def verify_step(self, tok: torch.Tensor, positions) -> torch.Tensor:
@@ -801,7 +773,6 @@ class Engine:
             g.pos.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
             self._forward_rows(g, 1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
         torch.cuda.synchronize()
-        self.check_handoffs()
         return hidden
 
     def layer_step(self, l: int, hidden: torch.Tensor, positions, T: int = 1) -> list:
@@ -819,7 +790,6 @@ class Engine:
             ops.sumsq16(b.h, out=b.psq)
             self._layer(l, g, b, trace=trace)
         torch.cuda.synchronize()
-        self.check_handoffs()
         return trace
 
     def prefill_hidden(self, input_ids, N: int = 1, probe=None):

@@ -35,16 +35,13 @@ SIGNATURES = {
                                       _f, _f, _i, _i, _i, _p]),
     "qwen_attn_decode_mfma_noalloc": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _f,
                                            _i, _i, _i, _p]),
-    "qwen_qkv_attn_workspace_bytes": (_ll, [_i, _i, _i]),
-    "qwen_qkv_attn_decode": (_i, [_p, _p, _p, _p, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _ll, _i, _i, _i, _i, _i,
-                                  _i, _i, _f, _i, _i, _p]),
     "qwen_sumsq16": (_i, [_p, _p, _i, _i, _p]),
     "qwen_linear_workspace_bytes": (_ll, [_i, _i, _i, _i]),
     "qwen_linear": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _i, _p, _ll, _p]),
     "qwen_linear_rect": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _p, _p, _i, _i, _i, _i, _i, _p, _ll, _p]),
     "qwen_gemv_lds_bytes": (_ll, [_i, _i, _i, _i, _i, _i]),
     "qwen_gemv": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _f, _p, _i, _p, _i, _i, _p]),
-    "qwen_gemv_rowmap": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _f, _p, _i, _p, _p, _i, _i, _i, _p]),
+    "qwen_gemv_rowmap": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _f, _p, _i, _p, _p, _i, _i, _p]),
     "qwen_lm_head_argmax": (_i, [_p, _p, _p, _f, _p, _i, _i, _i, _p, _p, _i, _i, _p]),
     "qwen_argmax_extract": (_i, [_p, _i, _p, _p]),
     "qwen_embed": (_i, [_p, _p, _p, _i, _p, _p, _p, _i, _ll, _i, _p]),

@@ -293,54 +293,6 @@ def attn_decode_mfma_noalloc(qkv, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, pos
 
 # ------------------------------------------------------- weights + GEMMs
 
-QKV_ATTN_SYNC_BYTES = 4096  # the hand-off words at the end of a qwen_qkv_attn_decode workspace
-QKV_ATTN_ERR_OFFSET = 2304  # the error word, from the start of those 4096 bytes (after 256 + 64 + 256 words)
-
-
-def qkv_attn_supported(B: int, Nkv: int, num_splits: int) -> bool:
-    """Whether ``qkv_attn_decode`` takes the shape (B <= 2, 8 KV heads, B * 8 * splits <= 64)."""
-    return _lib.query("qwen_qkv_attn_workspace_bytes", B, Nkv, num_splits) > 0
-
-
-def qkv_attn_workspace(B: int, Nkv: int, num_splits: int, device) -> torch.Tensor:
-    """Zeroed workspace of ``qkv_attn_decode`` (split partials, counters, hand-off words)."""
-    n = _lib.query("qwen_qkv_attn_workspace_bytes", B, Nkv, num_splits)
-    assert n > 0, f"qkv_attn_decode does not take B={B} Nkv={Nkv} splits={num_splits}"
-    return torch.zeros(n, dtype=torch.uint8, device=device)
-
-
-def qkv_attn_failed(workspace: torch.Tensor) -> bool:
-    """True if a launch on this workspace had a bounded wait expire or a workgroup on another XCD
-    than the hand-off assumes (synchronises)."""
-    base = workspace.numel() - QKV_ATTN_SYNC_BYTES + QKV_ATTN_ERR_OFFSET
-    return bool(workspace[base:base + 4].any())
-
-
-def qkv_attn_decode(x, w_qkv_rows, ln1, row_map, eps, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions,
-                    k_cache, v_cache, scale, num_splits, *, out, workspace, kv_cached: bool = False) -> torch.Tensor:
-    """RMSNorm + QKV projection and the decode attention of one token per sequence in one launch
-    (``qwen_qkv_attn_decode``): ``gemv(x, w_qkv_rows, norm_w=ln1, row_map=row_map, groups=8,
-    out=qkv)`` followed by ``attn_decode_mfma(qkv, ..., T=1, waves=8)``, bit for bit.
-    ``w_qkv_rows`` is the head-major QKV weight, ``row_map`` its rows' natural columns; ``out`` is
-    ``[B, 1, Nq * D]``. Check ``qkv_attn_failed(workspace)`` after the launches (a bounded wait
-    that expired leaves its output unwritten)."""
-    _gpu(x, w_qkv_rows, ln1, row_map, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, positions, k_cache, v_cache, out,
-         workspace)
-    B, H = x.shape
-    Bk, Nkv, CAP, D = k_cache.shape
-    Nq = qkv.shape[1] // D - 2 * Nkv
-    assert x.dtype == BF16 and x.is_contiguous() and Bk == B and v_cache.shape == k_cache.shape
-    assert w_qkv_rows.shape == ((Nq + 2 * Nkv) * D, H) and w_qkv_rows.is_contiguous()
-    assert qkv.shape == (B, (Nq + 2 * Nkv) * D) and qkv.is_contiguous() and out.shape == (B, 1, Nq * D)
-    assert row_map.dtype == torch.int32 and positions.dtype == torch.int32 and positions.numel() == B
-    _lib.call("qwen_qkv_attn_decode", x.data_ptr(), w_qkv_rows.data_ptr(), ln1.data_ptr(), row_map.data_ptr(),
-              float(eps), qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos_tab.data_ptr(),
-              sin_tab.data_ptr(), positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
-              workspace.data_ptr(), workspace.numel(), B, H, Nq, Nkv, D, CAP, cos_tab.shape[0], float(scale),
-              int(num_splits), ATTN_KV_CACHED if kv_cached else 0, _stream())
-    return out
-
-
 class TiledWeight:
     """A projection weight ``[N, K]`` stored in MFMA-B tiles (see ``include/qwen_hip.h``).
 
@@ -638,14 +590,13 @@ def gemv_config(M: int, N: int, K: int, epi: int, device=None) -> tuple[int, int
 
 def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, residual=None, silu_pair: bool = False,
          out: torch.Tensor | None = None, amax: torch.Tensor | None = None, cfg=None,
-         row_map: torch.Tensor | None = None, groups: int = 1) -> torch.Tensor:
+         row_map: torch.Tensor | None = None) -> torch.Tensor:
     """``x @ w.T`` for ``x [M <= 2, K]`` over a row-major ``w [N, K]`` (``gemm_fused.py:136-173``
     semantics): optional RMSNorm prologue (``norm_w``), residual or SwiGLU epilogue
     (``silu_pair``: ``w = cat(gate, up)`` rows, output ``[M, N/2]``), or, with ``amax``, the
     first-index argmax of the bf16 logits folded into the packed int64 keys (LM head).
     ``row_map`` (store epilogue only; int32 ``[N]``, a permutation): weight row ``i``'s output
-    goes to column ``row_map[i]``; ``groups``: the weight's rows form that many equal contiguous
-    groups, and workgroup ``g`` takes a share of group ``g % groups`` (the XCD it runs on).
+    goes to column ``row_map[i]``.
     """
     _gpu(x, w, norm_w, residual, out, amax)
     assert x.dtype == BF16 and x.dim() == 2 and x.is_contiguous()
@@ -682,7 +633,7 @@ def gemv(x: torch.Tensor, w: torch.Tensor, *, norm_w=None, eps: float = 0.0, res
         _gpu(row_map)
         assert epi == GEPI_STORE and row_map.dtype == torch.int32 and row_map.numel() == N and row_map.is_contiguous()
         _lib.call("qwen_gemv_rowmap", x.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K, N, _nullable(norm_w),
-                  float(eps), None, epi, None, row_map.data_ptr(), int(groups), int(grid), int(waves), _stream())
+                  float(eps), None, epi, None, row_map.data_ptr(), int(grid), int(waves), _stream())
     return amax if epi == GEPI_ARGMAX else out
 
 
