@@ -10,13 +10,20 @@ qkv and the attention output at the op bars (GEMM: atol 1e-2 / rtol 1/64,
 ``engine/engine.py:425-429``; attention: 2e-2, ``tests/test_torch_ref.py:264``), the residual
 stream after O and down, and the SwiGLU product, by relative error (the hidden-state bar,
 2e-2), plus the cache slot the step writes.
+
+Each run prints every stage's relative error twice: accumulated (the oracle's chain from the
+layer input) and local (the oracle's stage applied to the engine's own input of that stage), with
+the attention also against the reference kernel's arithmetic in the engine's block order
+(``R.attn_decode_flash``), which is where the layer's excess over the twin comes from.
 """
+
+import functools
 
 import pytest
 import torch
 
 from __graft_entry__ import write_random_model
-from helpers import assert_close
+from helpers import assert_close, engine_schedule
 from oracle import ref_torch as R
 from oracle.model import QWEN3_4B, CpuQwen3
 
@@ -68,6 +75,28 @@ def test_c1_single_layer_per_tensor(c1, seed):
     h1, n2 = R.add_rms_norm(hidden, R.linear(a.view(1, -1), w["w_o"]), w["ln2"], ref.eps)
     p = R.silu_mul(R.linear(n2, w["w_gu"]))
     h2 = (h1.float() + R.linear(p, w["w_down"]).float()).to(BF16)
+
+    # Per-stage errors: accumulated (oracle chain) and local (oracle stage on the engine's input).
+    b = eng.bufs(eng.state.groups[0], 1)
+    flash = functools.partial(R.attn_decode_flash, schedule=engine_schedule(b.splits, b.attn_waves, 1))
+    kc_e, vc_e = torch.zeros_like(ref.k_cache[0]), torch.zeros_like(ref.v_cache[0])
+    kc_e[:, :, :CTX], vc_e[:, :, :CTX] = k_pre, v_pre
+    q_l = R.qk_norm_rope_cache(got_qkv, w["q_norm"], w["k_norm"], ref.eps, ref.cos_tab, ref.sin_tab, pos, 1, kc_e, vc_e)
+    a_l = R.attn_decode(q_l, kc_e, vc_e, pos + 1, ref.scale)
+    a_f = flash(q_l, kc_e, vc_e, pos + 1, ref.scale)
+    h1_l, _ = R.add_rms_norm(hidden, R.linear(got_a.view(1, -1), w["w_o"]), w["ln2"], ref.eps)
+    p_l = R.silu_mul(R.linear(R.rms_norm(got_h1, w["ln2"], ref.eps), w["w_gu"]))
+    h2_l = (got_h1.float() + R.linear(got_p, w["w_down"]).float()).to(BF16)
+    rows = [("qkv", _rel(got_qkv, qkv), _rel(got_qkv, qkv)),
+            ("attention (twin)", _rel(got_a.view(1, -1), a.view(1, -1)), _rel(got_a.view(1, -1), a_l.view(1, -1))),
+            ("attention (engine's block order)", None, _rel(got_a.view(1, -1), a_f.view(1, -1))),
+            ("h after O + residual", _rel(got_h1, h1), _rel(got_h1, h1_l)),
+            ("SwiGLU product", _rel(got_p, p), _rel(got_p, p_l)),
+            ("layer output", _rel(got_h2, h2), _rel(got_h2, h2_l))]
+    print(f"\nc1 seed {seed}: relative error per stage (accumulated / local)")
+    for name, acc, loc in rows:
+        print(f"  {name:34s} {'-' if acc is None else f'{acc:.2e}':>9s} {loc:.2e}")
+    assert _rel(got_a.view(1, -1), a_f.view(1, -1)) <= 5e-3, "attention vs the engine's block order"
 
     assert_close(got_qkv, qkv, 1e-2, 1 / 64, "qkv")
     assert_close(got_a.view(1, -1), a.view(1, -1), 2e-2, 2e-2, "attention output")
