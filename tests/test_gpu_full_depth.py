@@ -1,5 +1,5 @@
 """Full-depth parity of the decode path: Qwen3-4B, 36 layers, random-init bf16 weights (seed 0,
-std 0.02), against the CPU oracle on the engine's own weights. Three configurations:
+std 0.02), against the CPU oracle on the engine's own weights. Four configurations:
 
 * c2: batch 1, 128-token prompts, 256 greedy steps; the M = 1 GEMVs and the
   one-split attention; RMSNorm gains 1, as ``Qwen3RMSNorm`` initialises them.
@@ -7,6 +7,9 @@ std 0.02), against the CPU oracle on the engine's own weights. Three configurati
   the 4-split attention (a 2048-slot capacity); RMSNorm gains 1 + N(0, 0.2) on all five norms.
 * c5's verify step: batch 4, periodic prompts, speculation k = 4 on every step (the T = 5, M = 20
   verify forward with 8-split attention at a 4096-slot capacity); the same non-unit gains.
+* c4's launch shapes: batch 32, 64-token prompts, 16 greedy steps; the M = 32 projections
+  (split-K skinny QKV / O / down, the rectangle gate/up) and the one-split attention; the same
+  non-unit gains.
 
 Greedy tokens follow the north-star rule, judged like the reference's judge
 (``tests/local_check.py:233-271``, ``:322-337``; speculation ``tests/spec_check.py:26-85``): the
@@ -25,8 +28,9 @@ cache copied into the oracle (so the prompt forward's error does not enter), com
   relative at every layer with the twin's attention (half the north-star 2e-2) and within 5e-3
   with the engine's attention block order;
 * accumulated: the oracle's whole step from the embedding against the engine's, within 1.25x the
-  reference kernel's own distance from the twin on the same step (+ 2e-3), and within that
-  distance (+ 2e-3) of the oracle run in the engine's block order.
+  floor (+ 2e-3), and within the floor (+ 2e-3) of the oracle run in the engine's block order. The
+  floor is the larger distance from the twin of two faithful reorderings of the reference's
+  arithmetic on the same step: the reference kernel's blocks, and the engine's.
 
 The oracle's weights are the engine's device weights copied to the host (the device generator is
 bit-identical to ``oracle/weights.py``: ``tests/test_gpu_ops.py``).
@@ -122,9 +126,11 @@ def check_hidden(name, eng, ref, prompt):
 
     * local error (the oracle's layer on the engine's input): <= 1e-2 with the twin's attention
       (half the north-star 2e-2), <= 5e-3 with the engine's attention block order;
-    * accumulated error: within 1.25x (+ 2e-3) of the reference kernel's own distance from the
-      twin against the twin, and within that distance (+ 2e-3) against the oracle run in the
-      engine's block order."""
+    * accumulated error: within 1.25x (+ 2e-3) of the floor against the twin, and within the floor
+      (+ 2e-3) against the oracle run in the engine's block order. The floor is the larger distance
+      from the twin of two faithful reorderings of the reference's arithmetic, both computed on the
+      CPU: the reference kernel's 64-key blocks, and the engine's 32-key blocks. (At contexts of
+      at most 64 keys the reference kernel's one block is the twin, and only the second is > 0.)"""
     B, Sp = len(prompt), len(prompt[0])
     list(eng.generate(prompt, 1))                                  # prompt forward + state
     tok = torch.tensor(prompt)[:, -1:]
@@ -163,11 +169,14 @@ def check_hidden(name, eng, ref, prompt):
         "accumulated, engine vs oracle (engine's block schedule)": [rel(hidden[l], acc["engine-sched"][l])
                                                                     for l in range(L)],
         "accumulated, reference kernel vs twin": [rel(acc["kernel"][l], acc["twin"][l]) for l in range(L)],
+        "accumulated, oracle in the engine's block order vs twin": [rel(acc["engine-sched"][l], acc["twin"][l])
+                                                                   for l in range(L)],
     }
     print(f"{name}: relative error per layer (splits {b.splits}, waves {b.attn_waves})")
     for k, v in rows.items():
         print(f"  {k:58s} " + " ".join(f"{r:.1e}" for r in v), flush=True)
-    floor = rows["accumulated, reference kernel vs twin"]
+    floor = [max(a, b) for a, b in zip(rows["accumulated, reference kernel vs twin"],
+                                       rows["accumulated, oracle in the engine's block order vs twin"])]
     bars = {"local, engine vs oracle (twin attention)": [1e-2] * L,
             "local, engine vs oracle (engine's block schedule)": [5e-3] * L,
             "accumulated, engine vs oracle (twin attention)": [1.25 * f + 2e-3 for f in floor],
@@ -257,6 +266,25 @@ def test_b8_full_depth_hidden_states(full_gains, monkeypatch):
     eng, ref = full_gains
     monkeypatch.setitem(engine_mod.CONFIG, "cap_round", 2048)
     check_hidden("c3 shapes B=8", eng, ref, _prompt(12, 8, 256))
+
+
+def test_b32_full_depth_greedy_tokens(full_gains):
+    """c4's decode launch shapes (M = 32: skinny QKV / O / down with split-K, the rectangle gate/up,
+    the M = 32 LM head, one-split attention over 32 sequences) through 36 layers."""
+    eng, ref = full_gains
+    B, Sp, Nn = 32, 64, 16
+    prompt = _prompt(13, B, Sp)
+    steps = list(eng.generate(prompt, Nn))
+    assert len(steps) == Nn and all(len(s) == B for s in steps)
+    b = eng.state.bufs[(0, 1)]
+    assert b.splits == 1 and not b.gemv and len(b.cfg["gu"]) == 4 and b.cfg["qkv"][2] > 1
+    tokens = [[steps[n][i] for n in range(Nn)] for i in range(B)]
+    check_tokens("c4 shapes B=32", ref, prompt, tokens)
+
+
+def test_b32_full_depth_hidden_states(full_gains):
+    eng, ref = full_gains
+    check_hidden("c4 shapes B=32", eng, ref, _prompt(14, 32, 64))
 
 
 def _periodic(period, n):

@@ -112,6 +112,41 @@ def test_attn_prefill_matches_oracle(qops, B, T, p0, Nkv):
     assert_close(got, want, 2e-2, 2e-2, f"attn_prefill B={B} T={T} p0={p0}")
 
 
+def _ulp_units(got, want):
+    """|got - want| in bf16 ulps of each element of ``want``, with magnitudes below 2^-6 of their
+    row's largest counted at that floor (so near-zero outputs do not inflate the count)."""
+    g, w = got.float(), want.float()
+    mag = torch.maximum(w.abs(), w.abs().amax(dim=-1, keepdim=True) * 2 ** -6).clamp_min(1e-30)
+    return (g - w).abs() / torch.exp2(torch.floor(torch.log2(mag)) - 7)
+
+
+@pytest.mark.parametrize("B,T,p0,Nkv", [(1, 5, 0, 8), (2, 16, 0, 2), (1, 100, 37, 8), (3, 64, 64, 2),
+                                        (2, 33, 500, 8), (1, 300, 1000, 1), (1, 17, 3, 8)])
+def test_attn_prefill_matches_reference_kernel_arithmetic(qops, B, T, p0, Nkv):
+    """Both prompt-attention kernels against the reference's online softmax walked the way they walk
+    it (64-key blocks from key 0, P rounded to bf16 against each query's running maximum:
+    ``R.attn_decode_flash`` with one lane). What differs is the exponential (the hardware exp2 of
+    (s - m) * scale * log2 e) and fp32 summation order, so outputs agree to a bf16 ulp on all but
+    a few elements, far inside the 2e-2 attention bar."""
+    g = torch.Generator().manual_seed(B * 1000 + T + p0 + 7)
+    D, CAP = 128, p0 + T + 40
+    Nq = 4 * Nkv
+    kc = _bf16(B, Nkv, CAP, D, gen=g)
+    vc = _bf16(B, Nkv, CAP, D, gen=g)
+    q = _bf16(B, T, Nq, D, gen=g, scale=2.0)
+    scale = D ** -0.5
+    got = qops.attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), p0, scale).cpu().reshape(B * T, -1)
+    lengths = torch.full((B,), p0 + T, dtype=torch.int32)
+    want = R.attn_decode_flash(q, kc, vc, lengths, scale, R.reference_schedule(1)).reshape(B * T, -1)
+    twin = R.attn_decode(q, kc, vc, lengths, scale).reshape(B * T, -1)
+    u, ut = _ulp_units(got, want), _ulp_units(got, twin)
+    frac1, frac2 = float((u > 0).float().mean()), float((u > 1).float().mean())
+    print(f"B={B} T={T} p0={p0}: vs reference kernel arithmetic max {float(u.max()):.1f} ulp, {frac1:.2e} of "
+          f"elements differ, {frac2:.2e} by > 1 ulp; vs the twin max {float(ut.max()):.1f} ulp, "
+          f"{float((ut > 0).float().mean()):.2e} differ")
+    assert frac1 <= 2e-2 and frac2 <= 1e-3 and float(u.max()) <= 4
+
+
 def test_attn_prefill_first_query_sees_only_slot_zero(qops):
     """Position 0 sees one key: its output is that key's value row exactly (softmax of one)."""
     g = torch.Generator().manual_seed(3)
