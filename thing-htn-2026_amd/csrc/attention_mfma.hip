@@ -113,18 +113,68 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int qq = lane >> 4, rr = lane & 15;
-  const long long bh = blockIdx.x;
-  const long long b = bh / p.Nkv;
-  const int kvh = (int)(bh - b * p.Nkv);
+  // Grid (Nkv, splits, B): the indices come straight from the workgroup id, so the position
+  // load needs only the kernel arguments (one memory round trip before it, not two).
+  const int kvh = blockIdx.x;
   const int split = blockIdx.y;
+  const long long b = blockIdx.z;
+  const long long bh = b * p.Nkv + kvh;
   const int T = p.T;
   const int R = T * MG;
   const int Nq = p.Nkv * MG;
   const int nheads = Nq + 2 * p.Nkv;
-  const long long pos0 = p.pos[b];
-  const int nold = (int)min((long long)p.CAP, max(0ll, pos0));  // cached keys [0, nold)
   const bf16_t* kbase = p.kc + bh * p.CAP * MD;
   const bf16_t* vbase = p.vc + bh * p.CAP * MD;
+
+  // ---- prologue. Every load a wavefront needs is issued first (rows clamped to valid ones,
+  // dropped later): the position-free ones, then those that need the position, then its first
+  // cached block; then the RMSNorm + RoPE work: one memory round trip after the position's,
+  // overlapped with the block's. Query row r (token r / 4, head r % 4) belongs to wavefront
+  // r % WPG, new key t to wavefront WPG - 1 - t % WPG.
+  constexpr int QPW = (MT * 16 + WPG - 1) / WPG;  // query rows per wavefront
+  constexpr int KPW = (8 + WPG - 1) / WPG;        // new keys per wavefront (T <= 8)
+  const bf16_t* ct = p.cos_tab;
+  const bf16_t* st = p.sin_tab;
+  // Prologue values: widened at the load with one query tile; with two they stay raw bf16 until
+  // the block's loads are issued behind a scheduling barrier (below), since loads complete in
+  // issue order and a gain load the compiler places after the block makes the RMSNorm wait for
+  // the whole block (measured: c5 288.8 -> 291.2 verify steps/s; the same order costs c2 0.2 %).
+  constexpr bool RAW = MT == 2;
+  using PV = std::conditional_t<RAW, bf16_t, float>;
+  auto ld = [](bf16_t v) -> PV { if constexpr (RAW) return v; else return bf2f(v); };
+  auto fv = [](PV v) -> float { if constexpr (RAW) return bf2f(v); else return v; };
+  // First the loads that need no position (this wavefront's q, k and v rows, the gains), so they
+  // are in flight while the position arrives; then the table rows and the first cached block.
+  PV qx[QPW][2], qcs[QPW][4], kx[KPW][2], kcs[KPW][4];
+  bf16_t kv[KPW][2];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int r = wave + i * WPG;
+    const int rc = r < R ? r : 0;
+    const int t = rc / MG, g = rc - t * MG;
+    const bf16_t* qr = p.qkv + ((b * T + t) * nheads + (long long)(kvh * MG + g)) * MD;
+    qx[i][0] = ld(qr[lane]);
+    qx[i][1] = ld(qr[lane + 64]);
+  }
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    const int t = (WPG - 1 - wave) + j * WPG;
+    const int tc = t < T ? t : 0;
+    const bf16_t* row = p.qkv + (b * T + tc) * nheads * MD;
+    const bf16_t* kr = row + (long long)(Nq + kvh) * MD;
+    const bf16_t* vrow = row + (long long)(Nq + p.Nkv + kvh) * MD;
+    kx[j][0] = ld(kr[lane]);
+    kx[j][1] = ld(kr[lane + 64]);
+    kv[j][0] = vrow[lane];
+    kv[j][1] = vrow[lane + 64];
+  }
+  const PV qg0r = ld(p.qnw[lane]), qg1r = ld(p.qnw[lane + 64]);
+  const PV kg0r = ld(p.knw[lane]), kg1r = ld(p.knw[lane + 64]);
+  __builtin_amdgcn_sched_barrier(0);  // the position is requested after these loads, in flight with them
+
+  const long long pos0 = p.pos[b];
+  const int nold = (int)min((long long)p.CAP, max(0ll, pos0));  // cached keys [0, nold)
+  auto tab_row = [&](int t) { return min((long long)p.P - 1, max(0ll, pos0 + t)) * MD; };
 
   // ---- key partition: old keys in blocks of 32 over (split, wavefront); the new-key
   // block goes to the last wavefront of the last split.
@@ -172,34 +222,11 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
   constexpr int DEPTH = (MT == 1 && WPG == 4) ? 2 : 1;
   KVBlock blkA, blkB;
 
-  // ---- prologue. Every load a wavefront needs is issued first (rows clamped to valid ones,
-  // dropped later), then its first cached block, then the RMSNorm + RoPE work: one memory
-  // round trip, overlapped with the block's. Query row r (token r / 4, head r % 4) belongs
-  // to wavefront r % WPG, new key t to wavefront WPG - 1 - t % WPG.
-  constexpr int QPW = (MT * 16 + WPG - 1) / WPG;  // query rows per wavefront
-  constexpr int KPW = (8 + WPG - 1) / WPG;        // new keys per wavefront (T <= 8)
-  const bf16_t* ct = p.cos_tab;
-  const bf16_t* st = p.sin_tab;
-  auto tab_row = [&](int t) { return min((long long)p.P - 1, max(0ll, pos0 + t)) * MD; };
-  // Prologue values: widened at the load with one query tile; with two they stay raw bf16 until
-  // the block's loads are issued behind a scheduling barrier (below), since loads complete in
-  // issue order and a gain load the compiler places after the block makes the RMSNorm wait for
-  // the whole block (measured: c5 288.8 -> 291.2 verify steps/s; the same order costs c2 0.2 %).
-  constexpr bool RAW = MT == 2;
-  using PV = std::conditional_t<RAW, bf16_t, float>;
-  auto ld = [](bf16_t v) -> PV { if constexpr (RAW) return v; else return bf2f(v); };
-  auto fv = [](PV v) -> float { if constexpr (RAW) return bf2f(v); else return v; };
-  PV qx[QPW][2], qcs[QPW][4], kx[KPW][2], kcs[KPW][4];
-  bf16_t kv[KPW][2];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
     const int r = wave + i * WPG;
     const int rc = r < R ? r : 0;
-    const int t = rc / MG, g = rc - t * MG;
-    const bf16_t* qr = p.qkv + ((b * T + t) * nheads + (long long)(kvh * MG + g)) * MD;
-    const long long tr = tab_row(t);
-    qx[i][0] = ld(qr[lane]);
-    qx[i][1] = ld(qr[lane + 64]);
+    const long long tr = tab_row(rc / MG);
     qcs[i][0] = ld(ct[tr + lane]);
     qcs[i][1] = ld(ct[tr + lane + 64]);
     qcs[i][2] = ld(st[tr + lane]);
@@ -208,22 +235,12 @@ attn_mfma_kernel(MfmaAttnParams p) {  // LDS holds one workgroup per CU: at most
 #pragma unroll
   for (int j = 0; j < KPW; ++j) {
     const int t = (WPG - 1 - wave) + j * WPG;
-    const int tc = t < T ? t : 0;
-    const bf16_t* row = p.qkv + (b * T + tc) * nheads * MD;
-    const bf16_t* kr = row + (long long)(Nq + kvh) * MD;
-    const bf16_t* vrow = row + (long long)(Nq + p.Nkv + kvh) * MD;
-    const long long tr = tab_row(tc);
-    kx[j][0] = ld(kr[lane]);
-    kx[j][1] = ld(kr[lane + 64]);
-    kv[j][0] = vrow[lane];
-    kv[j][1] = vrow[lane + 64];
+    const long long tr = tab_row(t < T ? t : 0);
     kcs[j][0] = ld(ct[tr + lane]);
     kcs[j][1] = ld(ct[tr + lane + 64]);
     kcs[j][2] = ld(st[tr + lane]);
     kcs[j][3] = ld(st[tr + lane + 64]);
   }
-  const PV qg0r = ld(p.qnw[lane]), qg1r = ld(p.qnw[lane + 64]);
-  const PV kg0r = ld(p.knw[lane]), kg1r = ld(p.knw[lane + 64]);
   if constexpr (RAW) __builtin_amdgcn_sched_barrier(0);
   load_block(blkA, wb0 * MKB);  // unconditional: a wavefront without blocks re-reads valid slots
   if constexpr (DEPTH == 2) load_block(blkB, (wb0 + BSTEP) * MKB);
@@ -636,7 +653,7 @@ int mfma_rows(int T) { return T <= 4 ? 16 : 32; }
 
 template <int MT>
 int launch_mfma(const MfmaAttnParams& p, int B, int waves, hipStream_t stream) {
-  dim3 grid((unsigned)((long long)B * p.Nkv), p.S);
+  dim3 grid((unsigned)p.Nkv, (unsigned)p.S, (unsigned)B);  // (KV head, split, sequence)
   if (waves == 4) {
     if (p.kv_cached) attn_mfma_kernel<MT, 4, true><<<grid, 256, 0, stream>>>(p);
     else attn_mfma_kernel<MT, 4, false><<<grid, 256, 0, stream>>>(p);
@@ -695,7 +712,7 @@ int mfma_args_status(const void* qkv, const void* q_norm_w, const void* k_norm_w
     return QWEN_ENULL;
   if (D != MD || Nkv <= 0 || Nq != MG * Nkv || T < 1 || T > 8 || B < 0 || CAP <= 0 || P <= 0) return QWEN_EARG;
   if (num_splits < 1 || num_splits > MERGE_MAX || (waves != 4 && waves != 8)) return QWEN_EARG;
-  if ((long long)B * Nkv > 0x7fffffffLL) return QWEN_EARG;
+  if ((long long)B * Nkv > 0x7fffffffLL || B > 65535) return QWEN_EARG;  // B is the grid's z extent
   return QWEN_OK;
 }
 
