@@ -84,7 +84,7 @@ int qwen_attn_decode_fused(const void* qkv, const void* q_norm_w, const void* k_
 long long qwen_attn_mfma_workspace_bytes(int B, int T, int Nkv, int num_splits);
 
 /* qwen_attn_decode_fused on the matrix cores: same operator, arguments and effects, for
- * 1 <= T <= 8 and 1 <= num_splits <= 8. One workgroup per (sequence, KV head, split) serves
+ * 1 <= T <= 8, 1 <= num_splits <= 8 and B <= 65535. One workgroup per (KV head, split, sequence) serves
  * all T * 4 query rows of the KV head (each cache byte read once per launch); QK^T and PV run
  * on v_mfma_f32_16x16x32_bf16; waves (4|8) wavefronts split each context split further.
  * Replaces engine/kernels/rope.py:169-226 followed by engine/kernels/attention.py:278-348
