@@ -120,9 +120,10 @@ def rel(a, b):
     return float((a - b).norm() / b.norm())
 
 
-def check_hidden(name, eng, ref, prompt):
-    """Hidden states after each layer for one decode step (the last prompt token re-run at its
-    position) over the engine's K/V; returns the per-layer relative errors. Bars, per layer:
+def check_hidden(name, eng, ref, prompt, T=1):
+    """Hidden states after each layer for one step over the engine's K/V: the last ``T`` prompt
+    tokens re-run at their positions (T = 1 a decode step, T > 1 the verify forward); returns the
+    per-layer relative errors. Bars, per layer:
 
     * local error (the oracle's layer on the engine's input): <= 1e-2 with the twin's attention
       (half the north-star 2e-2), <= 5e-3 with the engine's attention block order;
@@ -133,32 +134,33 @@ def check_hidden(name, eng, ref, prompt):
       at most 64 keys the reference kernel's one block is the twin, and only the second is > 0.)"""
     B, Sp = len(prompt), len(prompt[0])
     list(eng.generate(prompt, 1))                                  # prompt forward + state
-    tok = torch.tensor(prompt)[:, -1:]
-    pos = torch.full((B,), Sp - 1, dtype=torch.int32)
-    hidden = eng.step_hidden(tok, [Sp - 1] * B)                     # the engine's step, its own K/V
+    tok = torch.tensor(prompt)[:, -T:]
+    p0 = Sp - T
+    pos = torch.full((B,), p0, dtype=torch.int32)
+    hidden = eng.step_hidden(tok, [p0] * B)                        # the engine's step, its own K/V
     g = eng.state.groups[0]
-    b = eng.bufs(g, 1)
+    b = eng.bufs(g, T)
     assert b.mfma_attn and len(eng.state.groups) == 1
-    sched = engine_schedule(b.splits, b.attn_waves, 1)
+    sched = engine_schedule(b.splits, b.attn_waves, T)
     L = ref.L
     ref.prepare(B, eng.CAP)
-    for l in range(L):                                             # slots < Sp - 1: the engine's prompt K/V
-        ref.k_cache[l][:, :, :Sp - 1] = eng.state.kcache(l)[:, :, :Sp - 1].cpu()
-        ref.v_cache[l][:, :, :Sp - 1] = eng.state.vcache(l)[:, :, :Sp - 1].cpu()
+    for l in range(L):                                             # slots < p0: the engine's prompt K/V
+        ref.k_cache[l][:, :, :p0] = eng.state.kcache(l)[:, :, :p0].cpu()
+        ref.v_cache[l][:, :, :p0] = eng.state.vcache(l)[:, :, :p0].cpu()
     attns = {"twin": R.attn_decode, "kernel": R.attn_decode_flash,
              "engine-sched": functools.partial(R.attn_decode_flash, schedule=sched)}
     acc = {}
     for k, attn in attns.items():
         ref.attention = attn
         acc[k] = []
-        ref.step(tok, pos, 1, hidden=acc[k])
+        ref.step(tok, pos, T, hidden=acc[k])
     local = {"twin": [], "engine-sched": []}
     emb = ref.w["embed"][tok.reshape(-1)]
     for k in local:
         ref.attention = attns[k]
         for l in range(L):
             out = []
-            ref.layer(l, emb if l == 0 else hidden[l - 1].cpu(), None, pos, 1, B, hidden=out)
+            ref.layer(l, emb if l == 0 else hidden[l - 1].cpu(), None, pos, T, B, hidden=out)
             local[k].append(out[0])
     ref.attention = R.attn_decode
     rows = {
@@ -172,7 +174,7 @@ def check_hidden(name, eng, ref, prompt):
         "accumulated, oracle in the engine's block order vs twin": [rel(acc["engine-sched"][l], acc["twin"][l])
                                                                    for l in range(L)],
     }
-    print(f"{name}: relative error per layer (splits {b.splits}, waves {b.attn_waves})")
+    print(f"{name}: relative error per layer (T {T}, splits {b.splits}, waves {b.attn_waves})")
     for k, v in rows.items():
         print(f"  {k:58s} " + " ".join(f"{r:.1e}" for r in v), flush=True)
     floor = [max(a, b) for a, b in zip(rows["accumulated, reference kernel vs twin"],
@@ -285,6 +287,17 @@ def test_b32_full_depth_greedy_tokens(full_gains):
 def test_b32_full_depth_hidden_states(full_gains):
     eng, ref = full_gains
     check_hidden("c4 shapes B=32", eng, ref, _prompt(14, 32, 64))
+
+
+def test_spec_full_depth_hidden_states(full_gains, monkeypatch):
+    """c5's verify forward (T = 5 tokens per sequence, M = 20, 8-split attention at a 4096-slot
+    capacity) through 36 layers: hidden states at the bars of ``check_hidden``."""
+    import engine as engine_mod
+    eng, ref = full_gains
+    monkeypatch.setitem(engine_mod.CONFIG, "cap_round", 4096)
+    name = "c5 verify B=4 T=5"
+    rows = check_hidden(name, eng, ref, _prompt(15, 4, 96), T=5)
+    assert eng.bufs(eng.state.groups[0], 5).splits == 8 and len(rows) == 6
 
 
 def _periodic(period, n):

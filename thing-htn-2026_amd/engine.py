@@ -764,14 +764,17 @@ class Engine:
         return out
 
     def step_hidden(self, tok: torch.Tensor, positions) -> list:
-        """One eager decode step of ``tok [B, 1]`` at ``positions`` (prepared batch, one row
-        group); returns the residual stream after every layer."""
+        """One eager step of ``tok [B, T]`` (T = 1: a decode step; T > 1: the verify forward, token
+        ``t`` of row ``b`` at ``positions[b] + t``) on the prepared batch, one row group; returns
+        the residual stream ``[B * T, H]`` after every layer."""
         st = self.state
         g = st.groups[0]
+        T = tok.shape[1]
+        assert tok.shape[0] == st.B and len(st.groups) == 1 and st.B * T <= 32 and T <= 16
         hidden = []
         with torch.inference_mode():
             g.pos.copy_(torch.as_tensor(positions, dtype=torch.int32).reshape(-1).to(self.device))
-            self._forward_rows(g, 1, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
+            self._forward_rows(g, T, tok=tok.to(self.device, torch.int64).contiguous(), hidden=hidden)
         torch.cuda.synchronize()
         return hidden
 
