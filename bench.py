@@ -466,7 +466,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box in this build has a single MI355X; sequences "
-              f"would shard data-parallel, see DESIGN.md); got --gpus {args.gpus}", file=sys.stderr)
+              f"would shard data-parallel over GPUs, with no exchange while decoding); got --gpus {args.gpus}",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     import engine as engine_mod
