@@ -97,8 +97,8 @@ def parse():
     p.add_argument("--profile-sample", action="store_true",
                    help="run only the dominant kernel of --config (c2: gate/up GEMV, c4: attention) and a plain "
                         "1 GiB device copy, for rocprofv3 --pmc traffic runs; prints one JSON line")
-    p.add_argument("--profile-kernel", default="dominant", choices=["dominant", "o", "qkv"],
-                   help="with --profile-sample: the dominant kernel, or the O or QKV projection")
+    p.add_argument("--profile-kernel", default="dominant", choices=["dominant", "o", "qkv", "down"],
+                   help="with --profile-sample: the dominant kernel, or the O, QKV or down projection")
     return p.parse_args()
 
 
@@ -219,6 +219,35 @@ def time_o_proj(eng, torch, reps=3, T=1):
     nbytes = w0.nbytes + M * w0.K * 2 + 2 * M * w0.N * 2
     name = ("gemv_kernel<%d, %d, false, 1>" % (M, b.gemv_cfg["o"][1]) if b.gemv
             else ops.gemm_kernel_name(M, b.cfg["o"], False, ops.EPI_RES))
+    return avg, nbytes, name
+
+
+def time_down(eng, torch, reps=3, T=1):
+    """Average launch time of the down projection + residual (M = B * T rows, K = 9728), rotating
+    over the 36 layers' weights. Returns (seconds, algorithmic bytes, kernel name)."""
+    from qwen_hip import ops
+    b = eng.bufs(eng.state.groups[0], T)
+    h2 = b.h.clone()
+
+    def one(w):
+        if b.gemv:
+            ops.gemv(b.p, w.down_rows, residual=h2, out=h2, cfg=b.gemv_cfg["down"])
+        else:
+            ops.fused_linear(b.p, w.down, b.cfg["down"], residual=h2, out=h2, workspace=b.gemm_ws)
+
+    def sweep():
+        for w in eng.w.layers:
+            one(w)
+        return len(eng.w.layers)
+
+    sweep()
+    torch.cuda.synchronize()
+    avg = _events_time(torch, sweep, reps, torch.cuda.current_stream())
+    w0 = eng.w.layers[0].down
+    M = b.M
+    nbytes = w0.nbytes + M * w0.K * 2 + 2 * M * w0.N * 2
+    name = ("gemv_kernel<%d, %d, false, 1>" % (M, b.gemv_cfg["down"][1]) if b.gemv
+            else ops.gemm_kernel_name(M, b.cfg["down"], False, ops.EPI_RES))
     return avg, nbytes, name
 
 
@@ -441,11 +470,13 @@ def cpu_baseline(eng, cfg, S, runs=3, target_s=6.0):
 
 
 def profile_sample(eng, torch, config, kernel="dominant"):
-    """Dominant-kernel (or ``kernel="o"`` / ``"qkv"``: the O / QKV projection) launches at the config's
+    """Dominant-kernel (or ``kernel="o"`` / ``"qkv"`` / ``"down"``: that projection) launches at the config's
     step width, plus a copy of known size (the FETCH_SIZE / WRITE_SIZE calibration)."""
     T = SPEC_T if config == "c5" else 1
     if kernel == "o":
         avg, nbytes, name = time_o_proj(eng, torch, reps=1, T=T)
+    elif kernel == "down":
+        avg, nbytes, name = time_down(eng, torch, reps=1, T=T)
     elif kernel == "qkv":
         avg, nbytes, name = time_qkv(eng, torch, reps=1, T=T)
     elif config == "c4":
