@@ -9,7 +9,9 @@
 //
 // Work decomposition (CDNA4): one workgroup per (sequence, KV head, context split) serves
 // all R = T * 4 query rows of that KV head (the T query tokens x the 4 query heads), so
-// each cache byte is read once for all of them. Its wavefronts split the split's keys
+// each cache byte is read once for all of them. The grid is (KV head, split, sequence):
+// workgroup kvh + Nkv * (split + S * b) runs on XCD kvh mod 8 (with Nkv = 8, head h's
+// workgroups share XCD h with the M <= 2 QKV GEMV's workgroups that produce its rows). Its wavefronts split the split's keys
 // into blocks of 32. Per block and wavefront:
 //   S [16-row tiles x 32 keys] = Q K^T on v_mfma_f32_16x16x32_bf16: the A operand (Q) is
 //     staged once in LDS; the B operand (K^T) is loaded straight from the cache, lane
