@@ -249,6 +249,14 @@ def full_gains(tmp_path_factory):
     torch.cuda.empty_cache()
 
 
+def test_c2_full_depth_hidden_states_gains(full_gains):
+    """c2's M = 1 GEMV path (RMSNorm prologues with non-unit gains on all five norms, the
+    one-split attention) through 36 layers, at the bars of ``check_hidden``."""
+    eng, ref = full_gains
+    check_hidden("c2 non-unit gains", eng, ref, _prompt(16))
+    assert eng.bufs(eng.state.groups[0], 1).gemv
+
+
 def test_b8_full_depth_greedy_tokens(full_gains, monkeypatch):
     """c3's decode launch shapes (M = 8 MFMA projections, 4-split attention) through 36 layers."""
     import engine as engine_mod
